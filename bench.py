@@ -1,0 +1,183 @@
+"""bench.py -- MI355X throughput of r4dx's quantized-weight matrix-product path (BASELINE.json metric:
+trellis GEMV effective HBM GB/s at M = 1 over one 27B-class layer's projections).
+
+A step is one decode-time pass over config 1's ten projections at M = 1, KB = 4: for each, the input
+transform (f16 x -> f16 A) and the trellis GEMV with its FWHT/svh epilogue (bf16 out). The weights
+rotate over enough copies (> 1 GiB) that the 256 MB MALL cannot serve them, so every step reads its
+compressed weights from HBM. Inputs are resident in HBM before the timed region.
+
+value = compressed-weight bytes per step / step time. `roofline` is the GEMV kernel alone: its
+algorithmic bytes (weights + A + svh + C) over its average launch duration, timed with HIP events on
+the stream the kernel runs on. `cpu_baseline` is the CPU oracle (decode + fp64 linear) on a bounded
+sample, timed on this host. Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--kb", type=int, default=4)
+    ap.add_argument("--m", type=int, default=1)
+    ap.add_argument("--copies", type=int, default=0, help="weight copies (0: enough for > 1 GiB)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--kernel-only", action="store_true", help="only the GEMV launches (for rocprof)")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
+              "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    from r4dx_amd import api, workloads as WL
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    KB, M = args.kb, args.m
+    shapes = WL.LAYER_SHAPES
+    layer_wbytes = sum(K * N * KB // 8 for _, K, N in shapes)
+    copies = args.copies or max(2, int(np.ceil((1 << 30) / layer_wbytes)) + 1)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    lin = []
+    for i, (name, K, N) in enumerate(shapes):
+        nw = K * N * KB // 32
+        words = [torch.randint(-2**31, 2**31 - 1, (nw,), dtype=torch.int32, device=dev, generator=gen)
+                 for _ in range(copies)]
+        suh = torch.from_numpy(WL.signs(K, 10 + i)).to(dev)
+        svh = torch.from_numpy(WL.svh_scales(N, 20 + i)).to(dev)
+        x = torch.from_numpy(WL.activations_f16(M, K, 30 + i)).to(dev)
+        a = torch.empty((M, K), dtype=torch.float16, device=dev)
+        skg = api.trellis_gemv_skg(K, N, KB)
+        ws = torch.empty(max(1, skg * M * N), dtype=torch.float32, device=dev)
+        tickets = api.TicketBuffer(N, dev).t
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        lin.append(dict(name=name, K=K, N=N, words=words, suh=suh, svh=svh, x=x, a=a, skg=skg, ws=ws,
+                        tickets=tickets, out=out))
+    out_scale = float(np.float32(1.0 / np.sqrt(128.0)))
+    stream = torch.cuda.current_stream()
+
+    def gemv(L, copy):
+        api.trellis_gemm_m64(L["a"], L["words"][copy], L["svh"], L["K"], L["N"], KB, skg=L["skg"],
+                             out=L["out"], ws=L["ws"], tickets=L["tickets"], out_scale=out_scale,
+                             stream=stream)
+
+    def step(s):
+        c = s % copies
+        for L in lin:
+            if not args.kernel_only:
+                api.trellis_input(L["x"], [L["suh"]], 0, bf16=False, outs=[L["a"]], stream=stream)
+            gemv(L, c)
+
+    for L in lin:   # A once, so --kernel-only has valid inputs
+        api.trellis_input(L["x"], [L["suh"]], 0, bf16=False, outs=[L["a"]], stream=stream)
+    for s in range(args.warmup):
+        step(s)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for s in range(args.steps):
+        step(args.warmup + s)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = e0.elapsed_time(e1) / args.steps
+
+    # The dominant kernel alone: per shape, R back-to-back launches over rotating copies.
+    R = 20
+    gemv_ms, alg_bytes = 0.0, 0.0
+    per_shape = {}
+    for L in lin:
+        for c in range(copies):
+            gemv(L, c)
+        b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        b0.record(stream)
+        for r in range(R):
+            gemv(L, r % copies)
+        b1.record(stream)
+        torch.cuda.synchronize()
+        avg_ms = b0.elapsed_time(b1) / R
+        K, N = L["K"], L["N"]
+        ab = K * N * KB / 8 + M * K * 2 + M * N * 2 + 4 * N
+        gemv_ms += avg_ms
+        alg_bytes += ab
+        per_shape[L["name"]] = round(ab / (avg_ms * 1e-3) / 1e9, 1)
+    achieved = alg_bytes / (gemv_ms * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(KB)
+
+    value = layer_wbytes / (ms_step * 1e-3) / 1e9
+    line = {
+        "metric": "trellis GEMV effective HBM GB/s @M=1 (27B layer shapes, KB4)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (uniform random trellis words, +-1 Hadamard signs, log-normal svh, N(0,1) x)",
+        "config": {"workload": f"config1: 10 projections of one 27B-class layer, M={M}, KB={KB}, "
+                               f"{copies} rotating weight copies ({copies * layer_wbytes / 2**30:.2f} GiB)",
+                   "M": M, "KB": KB, "weight_bytes_per_step": layer_wbytes,
+                   "step": "input transform + trellis GEMV (FWHT/svh epilogue, bf16 out) per projection"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "tq_gemv_kernel", "avg_launch_us": round(gemv_ms * 1e3 / len(lin), 3),
+                     "per_shape_GBs": per_shape},
+        "cpu_baseline": cpu,
+        "wall_s": round(wall, 3),
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(KB):
+    """The CPU oracle's decode + fp64 linear of config 0 (K = N = 5120, M = 1) on all host cores."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    from r4dx_amd import workloads as WL
+    K = N = 5120
+    words, suh, svh = WL.trellis_linear(K, N, KB, 1)
+    x = WL.activations_f16(1, K, 2).view(np.uint16)
+    lib = O.lib()
+    cores = lib.r4o_max_threads()
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        a = O.transform_input(x, False, suh, 0)
+        q = O.decode_pair_grid(words, K, N, KB, 0)
+        O.linear_from_a(a, q, svh, 0, nthreads=0)
+        reps += 1
+        if time.perf_counter() - t0 > 10.0 or reps >= 20:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    return {"value": round(K * N * KB / 8 / dt / 1e9, 4), "unit": "GB/s", "cores": cores,
+            "kind": "port", "sample": f"config0 K=N=5120 KB={KB} M=1: transform + decode + fp64 linear, "
+                                      f"{reps} runs, {dt * 1e3:.1f} ms each"}
+
+
+if __name__ == "__main__":
+    main()

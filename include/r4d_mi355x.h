@@ -1,0 +1,65 @@
+/* r4d_mi355x.h -- the C ABI of libr4d_mi355x, the MI355X (gfx950) build of r4dx's quantized-weight
+ * matrix-product path.  Every entry keeps the name, argument order and meaning of the reference
+ * entry it replaces (cited per declaration, paths relative to the reference repository root), so the
+ * engine's callers (src/model/linear.cpp ApplyLinear via src/core/include/r4dx/core/r4d.hpp) bind it
+ * unchanged.  Device pointers and streams travel as int64_t, shapes as int.  Nothing on a launch
+ * path allocates or synchronises.  An illegal shape throws std::runtime_error from the GEMM entries
+ * (as the reference's do); every GEMM family also has a _check entry that returns NULL or a message
+ * (valid until the calling thread's next check) without launching.
+ *
+ * Tuning knobs of the reference signatures (WV, SK, MT, NP, U, NT, skw) are accepted and ignored:
+ * this build plans its own geometry.  SKG (the grid K split) is honoured, because the caller sizes
+ * ws by it; results depend on (K, N, KB, SKG) and never on M.
+ */
+#ifndef R4D_MI355X_H
+#define R4D_MI355X_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- trellis GEMV / skinny GEMM, M = 1..64 ----------------------------------------------------- */
+/* third_party/libr4d/r4d.h:372-375 r4d_gemm_trellis_nt_m64: C bf16 [M][N] =
+ * bf16((FWHT128(A_p(n) @ Q) * svh) * out_scale); A f16 [M][K] (a1 = 0: a0), W the pair-grid words,
+ * ws fp32 ws_bytes(M, N, SKG), tickets u32 [N/128] zeroed before first use (self-resetting). */
+void r4d_gemm_trellis_nt_m64(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
+                             int64_t ws, int64_t tickets, int M, int K, int N, int KB, int WV, int SK,
+                             int MT, int NP, int SKG, int U, int NT, float out_scale, int64_t stream);
+/* r4d.h:380-383 _raw: fp32 C [M][N] = A @ Q, no output transform (clk accepted, unused). */
+void r4d_gemm_trellis_nt_m64_raw(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t c, int64_t ws,
+                                 int64_t tickets, int M, int K, int N, int KB, int WV, int SK, int MT,
+                                 int NP, int SKG, int U, int NT, int64_t clk, int64_t stream);
+int    r4d_gemm_trellis_nt_m64_has_rate(int KB);                 /* r4d.h:384 */
+int    r4d_gemm_trellis_nt_m64_max_m(void);                      /* r4d.h:385 */
+size_t r4d_gemm_trellis_nt_m64_ws_bytes(int M, int N, int SKG);  /* r4d.h:386 */
+size_t r4d_gemm_trellis_nt_m64_tickets_bytes(int N);             /* r4d.h:387 */
+void   r4d_gemm_trellis_nt_m64_zero_tickets(int64_t tickets, size_t bytes, int64_t stream); /* r4d.h:389 */
+/* r4d.h:390-393: the whole decoded Q[K][N] f16 bits, bit-exact against the format's decode. */
+void   r4d_trellis_reconstruct_f16(int64_t w, int64_t q, int K, int N, int KB, int64_t stream);
+/* No reference counterpart (the reference checks inside the throwing entry, r4d_gemm_trellis_nt_m64.hip:
+ * 614-650): the legality rules of the two entries above without launching. */
+const char* r4d_gemm_trellis_nt_m64_check(int M, int K, int N, int n_split, int KB, int SKG, int full,
+                                          int have_svh, int have_ws);
+/* No reference counterpart (the reference reads gemm_tuning_table_trellis.inc): this build's SKG for
+ * a shape, the same for every M. */
+int    r4d_mi355x_trellis_gemv_skg(int K, int N, int KB);
+
+/* ---- input transform and FWHT (src/kernels/include/r4dx/kernels/kernels.h) --------------------- */
+/* kernels.h:110-128 r4dx_trellis_input_bf16: out[o][m,k] = f16(FWHT128(fp32(x) * suh[o])[k] * scale),
+ * scale = float(2^prescale_log2 / sqrt(128)); x bf16 [M][K]; suh / out: HOST arrays of nout device
+ * pointers. */
+void r4dx_trellis_input_bf16(int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh,
+                             const int64_t* out, int prescale_log2, int64_t stream);
+/* The same for an f16 x (BASELINE's fp16 activations); no reference counterpart, same contract. */
+void r4dx_trellis_input_f16(int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh,
+                            const int64_t* out, int prescale_log2, int64_t stream);
+/* kernels.h:192-197 r4dx_fwht128_f32: in-place unnormalised FWHT of each 128-float block (use_lds
+ * accepted: both butterflies are the same fp32 operations in the same order). */
+void r4dx_fwht128_f32(int64_t x, int64_t blocks, int use_lds, int64_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,82 @@
+"""Python mirrors of the C entry points, over torch device tensors.  Each call validates through the
+library's own _check entry (or the same rules) first, so an illegal shape raises ValueError here
+instead of an uncaught C++ exception crossing ctypes."""
+import ctypes as C
+
+import torch
+
+from .loader import lib
+
+
+def _p(t):
+    return 0 if t is None else t.data_ptr()
+
+
+def _stream(stream=None):
+    s = torch.cuda.current_stream() if stream is None else stream
+    return s.cuda_stream
+
+
+class TicketBuffer:
+    """The per-linear ticket words of the split GEMMs (zeroed once; every complete launch leaves
+    them zero)."""
+
+    def __init__(self, N, device="cuda"):
+        self.t = torch.zeros(max(1, N // 128), dtype=torch.int32, device=device)
+
+
+def trellis_gemv_skg(K, N, KB):
+    return lib().r4d_mi355x_trellis_gemv_skg(K, N, KB)
+
+
+def trellis_gemm_m64(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out=None, ws=None,
+                     tickets=None, out_scale=1.0, raw=False, stream=None):
+    """C = r4d_gemm_trellis_nt_m64 (bf16 [M][N]) or, raw=True, its _raw fp32 A @ Q."""
+    L = lib()
+    M = a0.shape[0]
+    skg = trellis_gemv_skg(K, N, KB) if skg is None else skg
+    n_split = N if n_split is None else n_split
+    if ws is None and skg > 1:
+        ws = torch.empty(L.r4d_gemm_trellis_nt_m64_ws_bytes(M, N, skg) // 4, dtype=torch.float32,
+                         device=a0.device)
+    if tickets is None and skg > 1:
+        tickets = TicketBuffer(N, a0.device).t
+    msg = L.r4d_gemm_trellis_nt_m64_check(M, K, N, n_split, KB, skg, 0 if raw else 1,
+                                          int(svh is not None), int(ws is not None and tickets is not None))
+    if msg:
+        raise ValueError(msg.decode())
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32 if raw else torch.bfloat16, device=a0.device)
+    st = _stream(stream)
+    if raw:
+        L.r4d_gemm_trellis_nt_m64_raw(_p(a0), _p(a1), n_split, _p(w), _p(out), _p(ws), _p(tickets),
+                                      M, K, N, KB, 0, 0, 0, 0, skg, 0, 0, 0, st)
+    else:
+        L.r4d_gemm_trellis_nt_m64(_p(a0), _p(a1), n_split, _p(w), _p(svh), _p(out), _p(ws), _p(tickets),
+                                  M, K, N, KB, 0, 0, 0, 0, skg, 0, 0, float(out_scale), st)
+    return out
+
+
+def trellis_reconstruct(w, K, N, KB, stream=None):
+    q = torch.empty((K, N), dtype=torch.int16, device=w.device)
+    lib().r4d_trellis_reconstruct_f16(_p(w), _p(q), K, N, KB, _stream(stream))
+    return q
+
+
+def trellis_input(x, suh_list, prescale=0, bf16=True, outs=None, stream=None):
+    M, K = x.shape
+    n = len(suh_list)
+    if not 1 <= n <= 3 or K % 128:
+        raise ValueError("nout must be 1..3 and K a multiple of 128")
+    if outs is None:
+        outs = [torch.empty((M, K), dtype=torch.float16, device=x.device) for _ in range(n)]
+    suh = (C.c_int64 * n)(*[s.data_ptr() for s in suh_list])
+    out = (C.c_int64 * n)(*[o.data_ptr() for o in outs])
+    f = lib().r4dx_trellis_input_bf16 if bf16 else lib().r4dx_trellis_input_f16
+    f(_p(x), M, K, n, suh, out, prescale, _stream(stream))
+    return outs
+
+
+def fwht128(x, stream=None):
+    lib().r4dx_fwht128_f32(_p(x), x.numel() // 128, 0, _stream(stream))
+    return x

@@ -1,0 +1,50 @@
+// r4d_host.h -- host-side helpers of libr4d_mi355x: the error contract of the reference's C ABI
+// (third_party/libr4d/r4d.h:30-31: an illegal shape throws std::runtime_error; the _check functions
+// return nullptr or a message that stays valid until the calling thread's next check) and launch
+// error reporting.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+
+namespace r4d {
+
+// The calling thread's last check message (what a _check entry returns a pointer to).
+inline std::string& check_slot() {
+  static thread_local std::string s;
+  return s;
+}
+// nullptr for "", else the message kept in this thread's slot.
+inline const char* check_result(const std::string& msg) {
+  if (msg.empty()) return nullptr;
+  check_slot() = msg;
+  return check_slot().c_str();
+}
+[[noreturn]] inline void fail(const char* entry, const std::string& msg) {
+  throw std::runtime_error(std::string("r4d ") + entry + ": " + msg);
+}
+inline void require(const char* entry, const std::string& msg) {
+  if (!msg.empty()) fail(entry, msg);
+}
+inline void launch_ok(const char* entry) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) fail(entry, std::string("launch failed: ") + hipGetErrorString(e));
+}
+inline bool pow2_in(int v, int lo, int hi) {
+  return v >= lo && v <= hi && (v & (v - 1)) == 0;
+}
+inline std::string str(long long v) { return std::to_string(v); }
+
+}  // namespace r4d
+
+// Arguments of one trellis GEMV launch (trellis_gemv.hip).
+struct r4d_gemv_args {
+  int64_t a0, a1;
+  int n_split;
+  int64_t w, svh, c, ws, tickets;
+  int M, K, N, KB, SKG, full;
+  float out_scale;
+  int64_t stream;
+};

@@ -1,0 +1,51 @@
+"""Loads libr4d_mi355x.so and declares the ctypes signatures of include/r4d_mi355x.h."""
+import ctypes as C
+import os
+import re
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libr4d_mi355x.so")
+HEADER = os.path.join(os.path.dirname(PKG), "include", "r4d_mi355x.h")
+
+I64, I32, F32, SZ, P = C.c_int64, C.c_int, C.c_float, C.c_size_t, C.c_void_p
+CSTR = C.c_char_p
+I64P = C.POINTER(C.c_int64)
+
+SIGS = {
+    "r4d_gemm_trellis_nt_m64": (None, [I64, I64, I32, I64, I64, I64, I64, I64] + [I32] * 11 + [F32, I64]),
+    "r4d_gemm_trellis_nt_m64_raw": (None, [I64, I64, I32, I64, I64, I64, I64] + [I32] * 11 + [I64, I64]),
+    "r4d_gemm_trellis_nt_m64_has_rate": (I32, [I32]),
+    "r4d_gemm_trellis_nt_m64_max_m": (I32, []),
+    "r4d_gemm_trellis_nt_m64_ws_bytes": (SZ, [I32, I32, I32]),
+    "r4d_gemm_trellis_nt_m64_tickets_bytes": (SZ, [I32]),
+    "r4d_gemm_trellis_nt_m64_zero_tickets": (None, [I64, SZ, I64]),
+    "r4d_trellis_reconstruct_f16": (None, [I64, I64, I32, I32, I32, I64]),
+    "r4d_gemm_trellis_nt_m64_check": (CSTR, [I32] * 9),
+    "r4d_mi355x_trellis_gemv_skg": (I32, [I32, I32, I32]),
+    "r4dx_trellis_input_bf16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
+    "r4dx_trellis_input_f16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
+    "r4dx_fwht128_f32": (None, [I64, I64, I32, I64]),
+}
+
+_lib = None
+
+
+def header_symbols():
+    """Every function name declared in include/r4d_mi355x.h."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(r4dx?_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build() "
+                               "(python -m r4dx_amd.build); there is no fallback path")
+        _lib = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGS.items():
+            f = getattr(_lib, name)
+            f.restype = res
+            f.argtypes = args
+    return _lib

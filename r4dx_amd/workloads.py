@@ -1,0 +1,49 @@
+"""Synthetic inputs of BASELINE.json's configs (numpy, seeded).  No network, no checkpoints: the
+trellis words are uniform random uint32 (every 32-bit word is a valid ring), the Hadamard signs are
+random +-1, and the channel scales are log-normal, exactly as the configs describe."""
+import numpy as np
+
+# Config 1 / 2: one 27B-class hybrid layer's projections, (name, K in, N out)
+LAYER_SHAPES = [
+    ("gdn.qkv", 5120, 10240),
+    ("gdn.z", 5120, 6144),
+    ("gdn.out", 6144, 5120),
+    ("attn.q", 5120, 6144),
+    ("attn.k", 5120, 1024),
+    ("attn.v", 5120, 1024),
+    ("attn.o", 6144, 5120),
+    ("mlp.gate", 5120, 17408),
+    ("mlp.up", 5120, 17408),
+    ("mlp.down", 17408, 5120),
+]
+
+
+def trellis_words(K, N, KB, seed):
+    rng = np.random.default_rng(seed)
+    return rng.integers(0, 2**32, size=K * N * KB // 32, dtype=np.uint64).astype(np.uint32)
+
+
+def signs(n, seed):
+    rng = np.random.default_rng(seed)
+    return np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float32)
+
+
+def svh_scales(N, seed):
+    """+-1 * lognormal(ln 0.01, 0.3), rounded to fp16 then widened (the container stores fp16)."""
+    rng = np.random.default_rng(seed)
+    s = np.where(rng.random(N) < 0.5, -1.0, 1.0) * rng.lognormal(np.log(0.01), 0.3, N)
+    return s.astype(np.float16).astype(np.float32)
+
+
+def activations_f16(M, K, seed, outlier_frac=0.0, outlier_scale=20.0):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    if outlier_frac > 0:
+        cols = rng.choice(K, max(1, int(round(K * outlier_frac))), replace=False)
+        x[:, cols] *= outlier_scale
+    return x.astype(np.float16)
+
+
+def trellis_linear(K, N, KB, seed):
+    """(words, suh, svh) of one trellis linear."""
+    return trellis_words(K, N, KB, seed), signs(K, seed + 1), svh_scales(N, seed + 2)

@@ -1,0 +1,46 @@
+"""CPU checks of the drop-in boundary: libr4d_mi355x.so loads without a GPU, exports every symbol
+include/r4d_mi355x.h declares, and its host-side legality rules answer without launching."""
+import ctypes as C
+
+import pytest
+
+from r4dx_amd import loader
+
+
+@pytest.fixture(scope="module")
+def L():
+    return loader.lib()
+
+
+def test_exports_every_declared_symbol(L):
+    names = loader.header_symbols()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(L, n), n
+        assert n in loader.SIGS, "no ctypes signature for " + n
+
+
+def test_gemv_checks(L):
+    ck = L.r4d_gemm_trellis_nt_m64_check
+    assert ck(1, 5120, 5120, 5120, 4, 16, 1, 1, 1) is None
+    assert b"M must be" in ck(65, 5120, 5120, 5120, 4, 1, 1, 1, 1)
+    assert b"multiples of 128" in ck(1, 5100, 5120, 5120, 4, 1, 1, 1, 1)
+    assert b"KB 6" in ck(1, 5120, 5120, 5120, 6, 1, 1, 1, 1)
+    assert b"SKG" in ck(1, 5120, 5120, 5120, 4, 3, 1, 1, 1)
+    assert b"ws and tickets" in ck(1, 5120, 5120, 5120, 4, 2, 1, 1, 0)
+    assert b"svh" in ck(1, 5120, 5120, 5120, 4, 1, 1, 0, 1)
+    assert b"n_split" in ck(1, 5120, 5120, 100, 4, 1, 1, 1, 1)
+    assert ck(1, 5120, 5120, 5120, 4, 1, 0, 0, 0) is None      # _raw needs no svh
+
+
+def test_sizes_and_rates(L):
+    assert L.r4d_gemm_trellis_nt_m64_ws_bytes(8, 5120, 4) == 4 * 8 * 5120 * 4
+    assert L.r4d_gemm_trellis_nt_m64_tickets_bytes(5120) == 40 * 4
+    assert L.r4d_gemm_trellis_nt_m64_max_m() == 64
+    assert [L.r4d_gemm_trellis_nt_m64_has_rate(k) for k in (2, 3, 4, 5, 6)] == [0, 1, 1, 1, 0]
+
+
+@pytest.mark.parametrize("K,N", [(5120, 5120), (5120, 1024), (17408, 5120), (5120, 17408), (6144, 5120)])
+def test_gemv_split_plan(L, K, N):
+    skg = L.r4d_mi355x_trellis_gemv_skg(K, N, 4)
+    assert skg >= 1 and (K // 16) % skg == 0 and (K // 16) // skg >= 8

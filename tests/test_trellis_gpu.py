@@ -1,0 +1,163 @@
+"""GPU parity of the trellis path (r4d_trellis_reconstruct_f16, r4dx_trellis_input_*,
+r4d_gemm_trellis_nt_m64 / _raw) against the CPU oracle, through the C ABI.
+
+Bars: the decode and the transform are bit-exact; the bf16 linear is bit-exact against the oracle's
+epilogue applied to the kernel's own fp32 sums; the fp32 sums are within 1e-3 relative error with a
+1e-4 * rms(row) floor of the oracle's fp64 sums (fp32 accumulation, f16 x f16 products exact)."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from r4dx_amd import workloads as WL
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():
+    pytest.skip("no GPU", allow_module_level=True)
+
+from r4dx_amd import api  # noqa: E402
+from gpu_util import banner, close_rel, dev, host_u16  # noqa: E402
+
+RAW_REL, RAW_FLOOR = 1e-3, 1e-4
+
+
+def _grid(K, N, KB, seed):
+    return WL.trellis_words(K, N, KB, seed)
+
+
+@pytest.mark.parametrize("KB,K,N", [(4, 128, 128), (4, 256, 384), (5, 256, 256), (3, 384, 128),
+                                    (4, 5120, 5120), (5, 1024, 2048), (4, 1040, 64)])
+def test_reconstruct_bit_exact(KB, K, N):
+    banner("reconstruct", KB, K, N)
+    g = _grid(K, N, KB, 100 + KB)
+    q_ref = O.decode_pair_grid(g, K, N, KB)
+    q = api.trellis_reconstruct(dev(g), K, N, KB)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u16(q), q_ref)
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("prescale", [0, 3, -5])
+def test_input_transform_bit_exact(bf16, prescale):
+    banner("input", bf16, prescale)
+    M, K = 5, 5120
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((M, K)) * 4).astype(np.float32)
+    xb = O.f32_to_bf16_bits(x) if bf16 else x.astype(np.float16).view(np.uint16)
+    s1, s2 = WL.signs(K, 1), WL.signs(K, 2)
+    outs = api.trellis_input(dev(xb), [dev(s1), dev(s2)], prescale, bf16)
+    torch.cuda.synchronize()
+    for s, o in zip((s1, s2), outs):
+        ref = O.transform_input(xb, bf16, s, prescale)
+        assert np.array_equal(host_u16(o), ref)
+
+
+def test_fwht128_matches_oracle():
+    banner("fwht128")
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((7, 128)).astype(np.float32)
+    t = api.fwht128(dev(x.copy()))
+    torch.cuda.synchronize()
+    ref = x.copy()
+    for r in ref:
+        O.lib().r4o_fwht128_f32(O.ptr(r))
+    assert np.array_equal(t.cpu().numpy(), ref)
+
+
+def _linear_case(K, N, KB, M, seed, skg=None, two_part=False):
+    words, suh, svh = WL.trellis_linear(K, N, KB, seed)
+    a0 = WL.activations_f16(M, K, seed + 5).view(np.uint16)
+    a1 = WL.activations_f16(M, K, seed + 6).view(np.uint16) if two_part else None
+    n_split = (N // 256) * 128 if two_part else N
+    return words, svh, a0, a1, n_split
+
+
+@pytest.mark.parametrize("KB,K,N,M,skg", [
+    (4, 128, 128, 1, 1), (4, 512, 256, 1, 4), (4, 512, 256, 3, 2), (5, 768, 384, 8, 3),
+    (3, 512, 128, 2, 1), (4, 1024, 512, 16, 8), (4, 1024, 256, 17, 4), (4, 512, 256, 64, 2),
+    (5, 512, 128, 40, 1), (4, 5120, 5120, 1, None), (5, 5120, 5120, 1, None), (4, 5120, 1024, 8, None),
+])
+def test_gemm_raw_and_full(KB, K, N, M, skg):
+    banner("gemm", KB, K, N, M, skg)
+    skg = api.trellis_gemv_skg(K, N, KB) if skg is None else skg
+    words, svh, a0, _, _ = _linear_case(K, N, KB, M, 10 * KB + M)
+    w_d, a_d, svh_d = dev(words), dev(a0), dev(svh)
+    tickets = api.TicketBuffer(N).t
+    raw = api.trellis_gemm_m64(a_d, w_d, None, K, N, KB, skg=skg, raw=True, tickets=tickets)
+    out_scale = np.float32(1.0 / np.sqrt(128.0))
+    full = api.trellis_gemm_m64(a_d, w_d, svh_d, K, N, KB, skg=skg, out_scale=out_scale, tickets=tickets)
+    torch.cuda.synchronize()
+    q = O.decode_pair_grid(words, K, N, KB)
+    ref = O.raw_sums(a0, q)
+    raw_h = raw.cpu().numpy()
+    assert close_rel(raw_h, ref, RAW_REL, RAW_FLOOR) <= 1.0
+    # the epilogue is bit-exact given the kernel's own sums
+    c_ref = O.epilogue_from_raw(raw_h, svh, out_scale)
+    assert np.array_equal(host_u16(full), c_ref)
+    # tickets are left zero by complete launches
+    assert int(tickets.abs().sum()) == 0
+    # and the linear is within bf16 rounding of the fp64 reference
+    y = O.linear_from_a(a0, q, svh, 0)
+    got = O.bf16_bits_to_f32(host_u16(full))
+    assert close_rel(got, y, 2.0**-8, 1e-3) <= 1.0
+
+
+def test_one_hot_rows_return_q():
+    """tests/kernels/test_trellis_decode.cpp:9-10: one-hot A rows read rows of Q bit for bit."""
+    banner("one-hot")
+    K, N, KB = 1024, 512, 4
+    words = _grid(K, N, KB, 5)
+    ks = [0, 1, 15, 16, 255, 511, 777, 1023]
+    a = np.zeros((len(ks), K), np.uint16)
+    for m, k in enumerate(ks):
+        a[m, k] = 0x3C00
+    raw = api.trellis_gemm_m64(dev(a), dev(words), None, K, N, KB, skg=4, raw=True)
+    torch.cuda.synchronize()
+    q = O.decode_pair_grid(words, K, N, KB)
+    got = raw.cpu().numpy()
+    for m, k in enumerate(ks):
+        assert np.array_equal(got[m], O.f16_bits_to_f32(q[k]))
+
+
+def test_row_identity_and_determinism():
+    """A row's bits do not depend on M or on the other rows (reference row identity rule,
+    src/model/linear.cpp:33-53), and repeated launches are bit-identical."""
+    banner("row-identity")
+    K, N, KB = 2048, 1024, 4
+    words, svh, a, _, _ = _linear_case(K, N, KB, 64, 77)
+    w_d, svh_d = dev(words), dev(svh)
+    skg = api.trellis_gemv_skg(K, N, KB)
+    full = {}
+    for M in (1, 2, 4, 8, 16, 17, 33, 64):
+        full[M] = host_u16(api.trellis_gemm_m64(dev(a[:M]), w_d, svh_d, K, N, KB, skg=skg, out_scale=0.5))
+    torch.cuda.synchronize()
+    for M, c in full.items():
+        assert np.array_equal(c, full[64][:M]), M
+    again = host_u16(api.trellis_gemm_m64(dev(a[:8]), w_d, svh_d, K, N, KB, skg=skg, out_scale=0.5))
+    assert np.array_equal(again, full[8])
+
+
+def test_two_part_split():
+    banner("two-part")
+    K, N, KB, M = 512, 512, 4, 4
+    words, svh, a0, a1, n_split = _linear_case(K, N, KB, M, 31, two_part=True)
+    raw = api.trellis_gemm_m64(dev(a0), dev(words), None, K, N, KB, skg=2, a1=dev(a1), n_split=n_split, raw=True)
+    torch.cuda.synchronize()
+    q = O.decode_pair_grid(words, K, N, KB)
+    ref = O.raw_sums(a0, q, a1=a1, n_split=n_split)
+    assert close_rel(raw.cpu().numpy(), ref, RAW_REL, RAW_FLOOR) <= 1.0
+
+
+@pytest.mark.parametrize("name,K,N", WL.LAYER_SHAPES)
+def test_config1_shapes_m1_m8(name, K, N):
+    """every projection of the 27B-class layer at KB 4 and 5, M 1 and 8."""
+    for KB in (4, 5):
+        banner("config1", name, K, N, KB)
+        words, svh, a, _, _ = _linear_case(K, N, KB, 8, hash(name) % 1000)
+        q = O.decode_pair_grid(words, K, N, KB)
+        ref = O.raw_sums(a, q)
+        w_d = dev(words)
+        for M in (1, 8):
+            raw = api.trellis_gemm_m64(dev(a[:M]), w_d, None, K, N, KB, raw=True)
+            torch.cuda.synchronize()
+            assert close_rel(raw.cpu().numpy(), ref[:M], RAW_REL, RAW_FLOOR) <= 1.0, (KB, M)
