@@ -22,13 +22,14 @@
 // that same element order. Nothing else is permuted; the output columns are put back in the epilogue.
 //
 // THE VALUE PATH per state (s in the high or low half of a 32-bit window W):
-//   y = v_mad_u32_u16(W.half, 0xD12D, 0)             s * 0xD12D, exact
-//   x = v_pk_mad_u16(W.half -> hi, 0x83DC:0, y)       hi16 += s * 0x83DC, lo16 untouched  => s * K mod 2^32
+//   s = W >> 16 or W & 0xFFFF                        (double-rate VALU on gfx950)
+//   x = v_mul_lo_u32(s, 0x83DCD12D)                  (single rate on gfx950, measured)
 //   two states -> v_sad_u8 / v_sad_hi_u8 seeded with 0x64006400: the exact f16 bits of 1024 + bytesum
 //   one v_pk_fma_f16 with f16(0x1EEE), f16(0xC931): both weights, one rounding each.
 // At KB = 4 one v_alignbit window holds the states of (m, j) and (m, j + 4) (the two columns), so 12
-// alignbits cover the lane's 32 states. The 32-bit multiply is split because v_mul_lo_u32 is a
-// quarter-rate instruction on CDNA.
+// alignbits cover the lane's 32 states. Measured on gfx950 (one full chip of waves): v_mul_lo_u32,
+// v_alignbit, v_sad_u8 and v_pk_fma_f16 issue at ~34 T lane-ops/s, v_and / v_lshrrev / v_add_u32
+// at ~58 T, so a state costs ~3.4 single-rate issue slots.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -65,26 +66,15 @@ __device__ __forceinline__ float r4_bf16_to_f32(unsigned short h) {
 }
 
 // ---- trellis value path -------------------------------------------------------------------------
-#define R4_MUL1_LO 0x0000D12Du
-#define R4_MUL1_HI_PK 0x83DC0000u   // 0x83DC in the high half, 0 in the low half
 #define R4_SAD_SEED 0x64006400u     // f16 1024.0 in both halves
 #define R4_KINV2 0x1EEE1EEEu
 #define R4_KBIAS2 0xC931C931u
 
-// x = s * 0x83DCD12D mod 2^32 for the state in the HIGH half of w.
-__device__ __forceinline__ unsigned r4_hash_hi(unsigned w) {
-  unsigned y, x;
-  asm("v_mad_u32_u16 %0, %1, %2, 0 op_sel:[1,0,0,0]" : "=v"(y) : "v"(w), "v"(R4_MUL1_LO));
-  asm("v_pk_mad_u16 %0, %1, %2, %3 op_sel_hi:[1,1,1]" : "=v"(x) : "v"(w), "v"(R4_MUL1_HI_PK), "v"(y));
-  return x;
-}
-// ... for the state in the LOW half of w.
-__device__ __forceinline__ unsigned r4_hash_lo(unsigned w) {
-  unsigned y, x;
-  asm("v_mad_u32_u16 %0, %1, %2, 0" : "=v"(y) : "v"(w), "v"(R4_MUL1_LO));
-  asm("v_pk_mad_u16 %0, %1, %2, %3 op_sel_hi:[0,1,1]" : "=v"(x) : "v"(w), "v"(R4_MUL1_HI_PK), "v"(y));
-  return x;
-}
+// x = s * 0x83DCD12D mod 2^32 for the state in the HIGH half of w: a double-rate shift isolates
+// the state and one full-rate v_mul_lo_u32 (not quarter rate on gfx950) forms the product.
+__device__ __forceinline__ unsigned r4_hash_hi(unsigned w) { return (w >> 16) * 0x83DCD12Du; }
+// ... for the state in the LOW half of w (a double-rate mask).
+__device__ __forceinline__ unsigned r4_hash_lo(unsigned w) { return (w & 0xFFFFu) * 0x83DCD12Du; }
 // Two hashes -> the packed f16 pair (x0's weight in the low half, x1's in the high half).
 __device__ __forceinline__ unsigned r4_cb_pair(unsigned x0, unsigned x1) {
   const unsigned s0 = __builtin_amdgcn_sad_u8(x0, 0u, R4_SAD_SEED);
@@ -200,21 +190,32 @@ __device__ __forceinline__ r4f4 r4_mfma16(r4h8 a, r4h8 b, r4f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Grid-wide handoff of split partial sums: every thread's global stores are made visible at agent
-// scope, then one thread takes a ticket; the block that completes the count finishes the group and
-// resets the ticket to zero (the reference's self-resetting protocol, third_party/libr4d/r4d.h:365-371).
-// Returns true in every thread of the last block.
+// Grid-wide handoff of split partial sums. The partials are written with r4_store_coherent (agent-
+// scope relaxed atomic stores: write-through past this XCD's L2) and read back with r4_load_coherent,
+// so no agent-scope fence -- which on gfx950 writes back or invalidates the whole L2 of the XCD, a
+// ~1 us serialisation per workgroup -- is needed: each thread waits for its own stores to be
+// acknowledged (the workgroup-scope release), the block meets at a barrier, one thread takes a
+// ticket; the block that completes the count finishes the group and resets the ticket to zero (the
+// reference's self-resetting protocol, third_party/libr4d/r4d.h:365-371). Returns true in every
+// thread of the last block.
+__device__ __forceinline__ void r4_store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float r4_load_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ bool r4_ticket_last(unsigned* ticket, unsigned contributors, int* flag_lds) {
-  __threadfence();
+  // every coherent store of this thread acknowledged before the barrier (the workgroup-scope fence
+  // alone emits no wait on gfx950)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned old = atomicAdd(ticket, 1u);
+    const unsigned old = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = old == contributors - 1;
-    if (last) atomicExch(ticket, 0u);
+    if (last) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *flag_lds = last ? 1 : 0;
   }
   __syncthreads();
-  const bool last = *flag_lds != 0;
-  if (last) __threadfence();
-  return last;
+  return *flag_lds != 0;
 }

@@ -21,93 +21,159 @@
 namespace {
 
 constexpr int kWaves = 4;                      // pairs per workgroup = one 128-column group
-constexpr int kThreads = kWaves * R4_WAVE;
 
 template <int KB>
 struct Words {
   unsigned w[KB + 1];   // [0] history, [1..KB] own words
 };
 
-// Loads the lane's ring words of block (pair, k-tile kt): own words KB c .. KB c + KB - 1 of tile t,
-// and the history word before them.
-template <int KB>
-__device__ __forceinline__ void load_words(Words<KB>& s, const unsigned* __restrict__ blk, int t, int c) {
-  const unsigned* tile = blk + t * 8 * KB;
-  if constexpr (KB == 4) {
-    const r4u4 v = *(const r4u4*)(tile + 4 * c);
-    s.w[1] = v[0]; s.w[2] = v[1]; s.w[3] = v[2]; s.w[4] = v[3];
-    s.w[0] = tile[(4 * c + 31) & 31];
-  } else {
-#pragma unroll
-    for (int i = 0; i <= KB; ++i) s.w[i] = tile[r4_lane_word<KB>(c, i)];
-  }
+#define R4_RSRC_FLAGS 0x00020000
+typedef __amdgpu_buffer_rsrc_t r4_rsrc;
+__device__ __forceinline__ r4_rsrc r4_make_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, R4_RSRC_FLAGS);
 }
 
-// The lane's two A fragments (h = 0, 1) of row r, k-tile kt: k 16kt + {0..3, 8..11} and {4..7, 12..15}.
-__device__ __forceinline__ void load_a(r4h8 (&af)[2], const unsigned short* __restrict__ arow, int kt) {
-  const r4u4 lo = *(const r4u4*)(arow + 16 * kt);
-  const r4u4 hi = *(const r4u4*)(arow + 16 * kt + 8);
+// Byte offsets, inside a (pair, k-tile) block, of the lane's own words (KB c .. KB c + KB - 1 of tile t)
+// and history word (KB c - 1 mod 8 KB); block q of a step sits q * 64 KB bytes further.
+template <int KB>
+struct LaneWords {
+  unsigned own, hist;
+  __device__ __forceinline__ LaneWords(int q, int t, int c) {
+    const unsigned tile = (unsigned)(q * 16 * KB + t * 8 * KB);
+    own = (tile + KB * c) * 4u;
+    hist = (tile + (KB * c - 1 + 8 * KB) % (8 * KB)) * 4u;
+  }
+};
+
+// One step's words of this lane from the slice buffer at step byte offset so (out of range -> 0).
+template <int KB>
+__device__ __forceinline__ void load_words(Words<KB>& s, r4_rsrc r, const LaneWords<KB>& lw, unsigned so) {
+  if constexpr (KB == 4) {
+    const r4u4 v = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(r, lw.own + so, 0, 0));
+    s.w[1] = v[0]; s.w[2] = v[1]; s.w[3] = v[2]; s.w[4] = v[3];
+  } else {
+#pragma unroll
+    for (int i = 0; i < KB; ++i) s.w[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(r, lw.own + so + 4 * i, 0, 0);
+  }
+  s.w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, lw.hist + so, 0, 0);
+}
+
+// A row's two fragments (h = 0, 1) of one k-tile from the row buffer at byte offset off:
+// k 16kt + {0..3, 8..11} and {4..7, 12..15}.
+__device__ __forceinline__ void load_a(r4h8 (&af)[2], r4_rsrc r, unsigned off) {
+  const r4u4 lo = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  const r4u4 hi = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0));
   const r4u4 f0 = {lo[0], lo[1], hi[0], hi[1]}, f1 = {lo[2], lo[3], hi[2], hi[3]};
   af[0] = __builtin_bit_cast(r4h8, f0);
   af[1] = __builtin_bit_cast(r4h8, f1);
 }
 
-template <int KB, int MT>
-struct Stage {
-  Words<KB> w;
-  r4h8 a[MT][2];
-};
+// Same, for the plain pointer form (the reconstruct kernel).
+template <int KB>
+__device__ __forceinline__ void load_words_ptr(Words<KB>& s, const unsigned* __restrict__ blk, int t, int c) {
+  const unsigned* tile = blk + t * 8 * KB;
+#pragma unroll
+  for (int i = 0; i <= KB; ++i) s.w[i] = tile[r4_lane_word<KB>(c, i)];
+}
 
-template <int KB, int MT>
-__global__ __launch_bounds__(kThreads) void tq_gemv_kernel(
+// Kernel geometry: a workgroup is NPW tile pairs x SK waves (NPW SK = 4 waves, 256 threads); the
+// SK waves of a pair split the workgroup's K slice into SK contiguous parts, SKG workgroups split K.
+// NPW = 1 is the split form (every 128-column group is finished by the last of its 4 SKG
+// contributors through ws and tickets); NPW = 4 covers a whole group and, at SKG = 1, finishes it
+// in the workgroup (no ws). Many short workgroups let the dispatcher balance the VALU-bound decode
+// over the CUs (measured better on gfx950 than a persistent grid). Weights are prefetched PF steps
+// ahead (a step is 4 k-tiles = one dwordx4 per lane) and issued before A is staged in LDS.
+constexpr int kRedParts = 8;         // the final slice sum is 8 interleaved runs, added in order
+constexpr int kRedRows = 4;          // rows of the final slice sum per pass
+
+template <int KB, int MT, int NPW, bool ALDS>
+__global__ __launch_bounds__(256) void tq_gemv_kernel(
     const unsigned short* __restrict__ A0, const unsigned short* __restrict__ A1, int n_split,
     const unsigned* __restrict__ W, const float* __restrict__ svh, void* __restrict__ Cv,
     float* __restrict__ ws, unsigned* __restrict__ tickets, int M, int K, int N, int SKG, int full,
     float out_scale) {
-  extern __shared__ float red[];               // [MT * 16][128] + flag
+  constexpr int PF = 4;
+  constexpr int NT = 256;
+  constexpr int SK = 4 / NPW;
+  constexpr int BLK = 16 * KB;                 // words per (pair, k-tile) block
+  extern __shared__ r4u4 lds_raw[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int group = blockIdx.x, ky = blockIdx.y;
-  const int pair = group * kWaves + wave;
+  const int pl = wave % NPW, ks = wave / NPW;
+  const int ky = blockIdx.y;
+  const int pair = blockIdx.x * NPW + pl;
+  const int group = (blockIdx.x * NPW) >> 2;
   const int KT = K >> 4, ktw = KT / SKG, kt0 = ky * ktw;
-  const int steps = (ktw + 3) >> 2;
   const unsigned short* __restrict__ A = group * 128 >= n_split ? A1 : A0;
   const int q = lane >> 4, t = (lane >> 3) & 1, c = lane & 7, mrow = lane & 15;
-  constexpr int BLK = 16 * KB;                 // words per (pair, k-tile) block
+
+  // Steps (4 k-tiles each) of the slice, split into SK contiguous parts of at most nsw steps.
+  const int steps_all = (ktw + 3) >> 2;
+  const int nsw = (steps_all + SK - 1) / SK;
+  const int st_beg = ks * nsw;
+  const int nst = max(0, min(nsw, steps_all - st_beg));
+  const int ktl_pad = SK * nsw * 4;            // k-tiles the LDS copy of A covers (zero past ktw)
+
+  // LDS: [A slice (ALDS) + zero block] [SK - 1 partial accumulators per pair] [M x 128 sums]
+  //      [8 x 4 x 128 reduce runs] [flag]
+  const size_t a_vec = ALDS ? (size_t)ktl_pad * M * 2 + 2 : 0;      // r4u4 units
+  r4u4* alds = lds_raw;
+  float* part_acc = (float*)(lds_raw + a_vec);                       // [(SK-1) * NPW][8 MT][64]
+  float* red = part_acc + (size_t)(SK - 1) * NPW * 8 * MT * 64;      // [M][128]
+  float* runs = red + (size_t)M * 128;                               // [8][4][128]
+  int* flag = (int*)(runs + (size_t)kRedParts * kRedRows * 128);
 
   const unsigned* __restrict__ wpair = W + ((size_t)pair * KT + kt0) * BLK;
-  const unsigned short* arow[MT];
-  bool arow_ok[MT];
+  const r4_rsrc wr = r4_make_rsrc(wpair, (unsigned)ktw * BLK * 4u);
+  const LaneWords<KB> lw(q, t, c);
+  constexpr unsigned kStepBytes = 4 * BLK * 4;
+  // A: LDS byte address of this lane's fragment pair at step 0 and its per-step stride (rows >= M
+  // read the zero block with stride 0); or, from global memory, a buffer over A with the row offset.
+  unsigned a_off[MT], a_stride[MT];
+  const r4_rsrc ar = r4_make_rsrc(A, (unsigned)((size_t)M * K * 2));
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
     const int r = i * 16 + mrow;
-    arow_ok[i] = r < M;
-    arow[i] = A + (size_t)(r < M ? r : 0) * K;
+    if constexpr (ALDS) {
+      a_off[i] = r < M ? (unsigned)(((st_beg * 4 + q) * M + r) * 32) : (unsigned)(ktl_pad * M * 32);
+      a_stride[i] = r < M ? (unsigned)(4 * M * 32) : 0u;
+    } else {
+      a_off[i] = r < M ? (unsigned)((size_t)r * K * 2 + (size_t)(kt0 + st_beg * 4 + q) * 32) : 0x80000000u;
+      a_stride[i] = 4 * 32;
+    }
   }
 
+  struct St {
+    Words<KB> w;
+    r4h8 a[ALDS ? 1 : MT][2];
+  };
+  // Step s of this wave (clamped to its last step, so a prefetch past the end re-reads a cached
+  // line instead of another wave's weights).
+  auto load = [&](St& s, int sidx) {
+    const int sc = min(sidx, nst - 1);
+    load_words<KB>(s.w, wr, lw, (unsigned)(st_beg + sc) * kStepBytes);
+    if constexpr (!ALDS) {
+      const bool ok = (st_beg + sc) * 4 + q < ktw;
+#pragma unroll
+      for (int i = 0; i < MT; ++i) load_a(s.a[i], ar, ok ? a_off[i] + (unsigned)sc * a_stride[i] : 0x80000000u);
+    }
+  };
   r4f4 acc[MT][2];
 #pragma unroll
   for (int i = 0; i < MT; ++i) acc[i][0] = acc[i][1] = (r4f4){0.f, 0.f, 0.f, 0.f};
-
-  auto load = [&](Stage<KB, MT>& s, int st) {
-    const int ktl = st * 4 + q;                // k-tile inside the slice
-    const bool ok = ktl < ktw;
-    if (ok) {
-      load_words<KB>(s.w, wpair + (size_t)ktl * BLK, t, c);
-    } else {
-#pragma unroll
-      for (int i = 0; i <= KB; ++i) s.w.w[i] = 0u;
-    }
+  auto compute = [&](const St& s, int sidx) {
+    r4h8 af[MT][2];
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
-      if (ok && arow_ok[i]) {
-        load_a(s.a[i], arow[i], kt0 + ktl);
+      if constexpr (ALDS) {
+        const r4u4* p = (const r4u4*)((const char*)alds + a_off[i] + (unsigned)sidx * a_stride[i]);
+        af[i][0] = __builtin_bit_cast(r4h8, p[0]);
+        af[i][1] = __builtin_bit_cast(r4h8, p[1]);
       } else {
-        s.a[i][0] = s.a[i][1] = (r4h8){0, 0, 0, 0, 0, 0, 0, 0};
+        af[i][0] = s.a[i][0];
+        af[i][1] = s.a[i][1];
       }
     }
-  };
-  auto compute = [&](const Stage<KB, MT>& s) {
     unsigned d[2][2][4];
     r4_decode<KB>(s.w.w, d);
 #pragma unroll
@@ -115,48 +181,97 @@ __global__ __launch_bounds__(kThreads) void tq_gemv_kernel(
       const r4h8 b0 = r4_frag(d[0][h]), b1 = r4_frag(d[1][h]);
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
-        acc[i][0] = r4_mfma16(s.a[i][h], b0, acc[i][0]);
-        acc[i][1] = r4_mfma16(s.a[i][h], b1, acc[i][1]);
+        acc[i][0] = r4_mfma16(af[i][h], b0, acc[i][0]);
+        acc[i][1] = r4_mfma16(af[i][h], b1, acc[i][1]);
       }
     }
   };
 
-  {
-    Stage<KB, MT> s0, s1;
-    load(s0, 0);
-    int st = 0;
-    for (; st + 1 < steps; st += 2) {
-      load(s1, st + 1);
-      compute(s0);
-      if (st + 2 < steps) load(s0, st + 2);
-      compute(s1);
+  // The weight stream starts before A is staged, so its latency overlaps the staging.
+  St ring[PF];
+  if (nst > 0) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) load(ring[i], i);
+  }
+  if constexpr (ALDS) {
+    // chunk (ktl, row, j): k 16 (kt0 + ktl) + 8j .. + 8 of A[row] -> halves of fragments h = 0, 1;
+    // k-tiles past the slice are zero, and so is the 32-byte block after the copy (rows >= M read it).
+    const int chunks = ktl_pad * M * 2;
+    for (int i = threadIdx.x; i < chunks + 2; i += NT) {
+      r4u4 v = {0u, 0u, 0u, 0u};
+      const int j = i & 1, rm = i >> 1, r = rm % M, ktl = rm / M;
+      if (i < chunks && ktl < ktw) v = *(const r4u4*)(A + (size_t)r * K + 16 * (kt0 + ktl) + 8 * j);
+      r4u2* dst = (r4u2*)(alds + (size_t)rm * 2);
+      dst[j] = (r4u2){v[0], v[1]};        // h = 0, elements 4j .. 4j + 3
+      dst[2 + j] = (r4u2){v[2], v[3]};    // h = 1
     }
-    if (st < steps) compute(s0);
+    __syncthreads();
+  }
+  if (nst > 0) {
+    int st = 0;
+    for (; st + PF <= nst; st += PF) {
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        compute(ring[i], st + i);
+        load(ring[i], st + i + PF);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PF - 1; ++i)
+      if (st + i < nst) compute(ring[i], st + i);
   }
 
-  // Lane l holds rows 16 i + 4 (l >> 4) + j of column slot nb = l & 15 of fragment cs: true column
-  // 32 pair + 16 (nb >> 3) + (nb & 7) + 8 cs.
+  // Combine the SK waves of each pair in k order (ks = 0, 1, ...) into wave ks = 0.
+  if constexpr (SK > 1) {
+    if (ks > 0) {
+      float* dst = part_acc + ((size_t)((ks - 1) * NPW + pl) * 8 * MT) * 64;
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dst[((i * 2 + f) * 4 + j) * 64 + lane] = acc[i][f][j];
+    }
+    __syncthreads();
+    if (ks == 0) {
+#pragma unroll
+      for (int s = 1; s < SK; ++s) {
+        const float* src = part_acc + ((size_t)((s - 1) * NPW + pl) * 8 * MT) * 64;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][f][j] += src[((i * 2 + f) * 4 + j) * 64 + lane];
+      }
+    }
+  }
+
+  // Lane l of wave (pl, ks = 0) holds rows 16 i + 4 (l >> 4) + j of column slot nb = l & 15 of
+  // fragment cs: true column 32 pair + 16 (nb >> 3) + (nb & 7) + 8 cs.
   const int nb = lane & 15, rq = lane >> 4;
-  const int colp = 16 * (nb >> 3) + (nb & 7);  // + 8 cs, inside the pair
-  const int gcol0 = wave * 32 + colp;          // inside the group
+  const int gcol0 = (pair & 3) * 32 + 16 * (nb >> 3) + (nb & 7);   // inside the group
   float* Cf = (float*)Cv;
   unsigned short* Cb = (unsigned short*)Cv;
   const int n0 = group * 128;
+  const bool in_block = NPW == 4 && SKG == 1;   // the workgroup holds its whole group
 
   if (SKG == 1 && !full) {
+    if (ks == 0) {
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+      for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 16 * i + 4 * rq + j;
-        if (r < M) {
-          Cf[(size_t)r * N + n0 + gcol0] = acc[i][0][j];
-          Cf[(size_t)r * N + n0 + gcol0 + 8] = acc[i][1][j];
+        for (int j = 0; j < 4; ++j) {
+          const int r = 16 * i + 4 * rq + j;
+          if (r < M) {
+            Cf[(size_t)r * N + n0 + gcol0] = acc[i][0][j];
+            Cf[(size_t)r * N + n0 + gcol0 + 8] = acc[i][1][j];
+          }
         }
-      }
+    }
     return;
   }
-  if (SKG == 1) {
+  if (in_block) {
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -169,34 +284,58 @@ __global__ __launch_bounds__(kThreads) void tq_gemv_kernel(
       }
     __syncthreads();
   } else {
-    float* wsy = ws + (size_t)ky * M * N;
+    if (ks == 0) {
+      float* wsy = ws + (size_t)ky * M * N;
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+      for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = 16 * i + 4 * rq + j;
-        if (r < M) {
-          wsy[(size_t)r * N + n0 + gcol0] = acc[i][0][j];
-          wsy[(size_t)r * N + n0 + gcol0 + 8] = acc[i][1][j];
+        for (int j = 0; j < 4; ++j) {
+          const int r = 16 * i + 4 * rq + j;
+          if (r < M) {
+            r4_store_coherent(&wsy[(size_t)r * N + n0 + gcol0], acc[i][0][j]);
+            r4_store_coherent(&wsy[(size_t)r * N + n0 + gcol0 + 8], acc[i][1][j]);
+          }
         }
+    }
+    if (!r4_ticket_last(&tickets[group], (unsigned)(SKG * (4 / NPW)), flag)) return;
+    // Sum the SKG slices: run p (0..7) adds slices p, p + 8, ... in order; the 8 runs are then added
+    // in order 0..7 -- the same arithmetic for every element whatever M is. kRedRows rows at a time
+    // (bounded LDS); the finished sums land in red[r][128] for the epilogue.
+    const size_t sy = (size_t)M * N;
+    for (int r0 = 0; r0 < M; r0 += kRedRows) {
+      const int rows = min(kRedRows, M - r0);
+      for (int idx = threadIdx.x; idx < kRedParts * rows * 128; idx += NT) {
+        const int p = idx / (rows * 128), e = idx - p * rows * 128;
+        const int r = r0 + (e >> 7), col = e & 127;
+        const float* src = ws + (size_t)r * N + n0 + col;
+        float v = 0.f;
+        for (int y = p; y < SKG; y += 8 * kRedParts) {
+          float tv[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int yy = y + u * kRedParts;
+            tv[u] = yy < SKG ? r4_load_coherent(src + (size_t)yy * sy) : 0.f;
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v += tv[u];
+        }
+        runs[(size_t)p * kRedRows * 128 + e] = v;
       }
-    int* flag = (int*)(red + MT * 16 * 128);
-    if (!r4_ticket_last(&tickets[group], (unsigned)SKG, flag)) return;
-    // Sum the SKG partials in slice order.
-    for (int idx = threadIdx.x; idx < M * 128; idx += kThreads) {
-      const int r = idx >> 7, col = idx & 127;
-      const float* p = ws + (size_t)r * N + n0 + col;
-      float v = p[0];
-      for (int y = 1; y < SKG; ++y) v += p[(size_t)y * M * N];
-      if (full) red[idx] = v;
-      else Cf[(size_t)r * N + n0 + col] = v;
+      __syncthreads();
+      for (int e = threadIdx.x; e < rows * 128; e += NT) {
+        float v = runs[e];
+#pragma unroll
+        for (int p = 1; p < kRedParts; ++p) v += runs[(size_t)p * kRedRows * 128 + e];
+        if (full) red[(size_t)r0 * 128 + e] = v;
+        else Cf[(size_t)(r0 + (e >> 7)) * N + n0 + (e & 127)] = v;
+      }
+      __syncthreads();
     }
     if (!full) return;
-    __syncthreads();
   }
   // The epilogue: one wave per row, the group's 128 sums as (lane, lane + 64).
   const float sv0 = svh[n0 + lane], sv1 = svh[n0 + lane + 64];
-  for (int r = wave; r < M; r += kWaves) {
+  for (int r = wave; r < M; r += 4) {
     float v0 = red[r * 128 + lane], v1 = red[r * 128 + lane + 64];
     r4_fwht128_wave(v0, v1, lane);
     const float y0 = v0 * sv0, y1 = v1 * sv1;
@@ -219,7 +358,7 @@ __global__ __launch_bounds__(256) void tq_reconstruct_kernel(const unsigned* __r
   const int kt = st * 4 + q;
   if (kt >= KT) return;
   Words<KB> s;
-  load_words<KB>(s, W + ((size_t)pair * KT + kt) * (16 * KB), t, c);
+  load_words_ptr<KB>(s, W + ((size_t)pair * KT + kt) * (16 * KB), t, c);
   unsigned d[2][2][4];
   r4_decode<KB>(s.w, d);
 #pragma unroll
@@ -235,22 +374,48 @@ __global__ __launch_bounds__(256) void tq_reconstruct_kernel(const unsigned* __r
   }
 }
 
-template <int KB, int MT>
+// Dynamic LDS of one launch.
+size_t gemv_ktl_pad(int SK, int ktw) { return (size_t)SK * ((((ktw + 3) >> 2) + SK - 1) / SK) * 4; }
+size_t gemv_lds(int MT, int NPW, bool alds, int ktw, int M) {
+  const int SK = 4 / NPW;
+  return (alds ? gemv_ktl_pad(SK, ktw) * M * 32 + 32 : 0) + (size_t)(SK - 1) * NPW * 8 * MT * 64 * 4 +
+         (size_t)(M + kRedParts * kRedRows) * 128 * 4 + 16;
+}
+constexpr size_t kAldsMax = 48 * 1024;   // A slices up to this many bytes are staged in LDS
+
+template <int KB, int MT, int NPW, bool ALDS>
 void launch_gemv(const r4d_gemv_args& a) {
-  dim3 grid(a.N / 128, a.SKG), block(kThreads);
-  const size_t smem = (size_t)MT * 16 * 128 * sizeof(float) + 16;
-  hipLaunchKernelGGL((tq_gemv_kernel<KB, MT>), grid, block, smem, (hipStream_t)a.stream,
+  dim3 grid(a.N / 32 / NPW, a.SKG), block(256);
+  const int ktw = a.K / 16 / a.SKG;
+  const size_t smem = gemv_lds(MT, NPW, ALDS, ktw, a.M);
+  if (smem > 160 * 1024) r4d::fail("gemm_trellis_nt_m64", "LDS request above 160 KiB");
+  hipLaunchKernelGGL((tq_gemv_kernel<KB, MT, NPW, ALDS>), grid, block, smem, (hipStream_t)a.stream,
                      (const unsigned short*)a.a0, (const unsigned short*)(a.a1 ? a.a1 : a.a0), a.n_split,
                      (const unsigned*)a.w, (const float*)a.svh, (void*)a.c, (float*)a.ws,
                      (unsigned*)a.tickets, a.M, a.K, a.N, a.SKG, a.full, a.out_scale);
 }
 
+template <int KB, int MT, int NPW>
+void launch_gemv_a(const r4d_gemv_args& a) {
+  const int ktw = a.K / 16 / a.SKG;
+  if (gemv_ktl_pad(4 / NPW, ktw) * a.M * 32 <= kAldsMax) launch_gemv<KB, MT, NPW, true>(a);
+  else launch_gemv<KB, MT, NPW, false>(a);
+}
+
+// The split form (one pair per workgroup) whenever ws is there; the whole-group form for an
+// unsplit launch without ws.
+template <int KB, int MT>
+void launch_gemv_np(const r4d_gemv_args& a) {
+  if (a.SKG == 1 && (a.ws == 0 || a.tickets == 0)) launch_gemv_a<KB, MT, 4>(a);
+  else launch_gemv_a<KB, MT, 1>(a);
+}
+
 template <int KB>
 void launch_gemv_kb(const r4d_gemv_args& a) {
   const int mt = (a.M + 15) / 16;
-  if (mt <= 1) launch_gemv<KB, 1>(a);
-  else if (mt <= 2) launch_gemv<KB, 2>(a);
-  else launch_gemv<KB, 4>(a);
+  if (mt <= 1) launch_gemv_np<KB, 1>(a);
+  else if (mt <= 2) launch_gemv_np<KB, 2>(a);
+  else launch_gemv_np<KB, 4>(a);
 }
 
 }  // namespace
@@ -330,19 +495,27 @@ void r4d_trellis_reconstruct_f16(int64_t w, int64_t q, int K, int N, int KB, int
   r4d::launch_ok(entry);
 }
 
-// This build's split choice for the GEMV: the smallest divisor SKG of K/16 that puts at least 512
-// workgroups (two per CU) on the chip while every slice keeps >= 8 k-tiles; independent of M, so
-// every M <= 64 gets the same row bits.
+// This build's split choice for the GEMV: a workgroup is one tile pair x 4 waves, each wave taking
+// whole 4-k-tile steps. SKG is picked among the divisors of K/16 (at most 32: the last workgroup of a
+// group sums the slices): first whole steps for every wave, then >= 4 steps per wave (the
+// per-workgroup setup and reduction amortised), then >= 1024 workgroups, then the most slices.
+// Independent of M, so every M <= 16 gets the same row bits.
 int r4d_mi355x_trellis_gemv_skg(int K, int N, int KB) {
   (void)KB;
-  const int KT = K / 16, groups = N / 128;
-  if (KT <= 0 || groups <= 0) return 1;
-  int best = 1;
-  for (int d = 1; d <= 64 && d <= KT; ++d) {
+  const int KT = K / 16, pairs = N / 32;
+  if (KT <= 0 || pairs <= 0) return 1;
+  int best = 1, best_score = -1;
+  for (int d = 1; d <= 32 && d <= KT; ++d) {
     if (KT % d) continue;
-    if (KT / d < 8) break;
-    best = d;
-    if (groups * d >= 512) break;
+    const int ktw = KT / d;
+    const int whole = ktw % 16 == 0;
+    const int steps = (ktw + 15) / 16;        // per wave
+    const long long wgs = (long long)pairs * d;
+    const int score = whole * 8 + (steps >= 4) * 4 + (wgs >= 1024) * 2 + (wgs >= 512);
+    if (score > best_score || (score == best_score && d > best)) {
+      best = d;
+      best_score = score;
+    }
   }
   return best;
 }

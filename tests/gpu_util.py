@@ -16,6 +16,8 @@ def dev(a):
 
 
 def host_u16(t):
+    if t.dtype in (torch.bfloat16, torch.float16):
+        t = t.view(torch.int16)
     return t.cpu().numpy().view(np.uint16)
 
 

@@ -120,19 +120,20 @@ def test_one_hot_rows_return_q():
 
 
 def test_row_identity_and_determinism():
-    """A row's bits do not depend on M or on the other rows (reference row identity rule,
-    src/model/linear.cpp:33-53), and repeated launches are bit-identical."""
+    """For M <= 16 a row's bits do not depend on M or on the other rows (the reference's row identity
+    rule, src/model/linear.cpp:33-53, third_party/libr4d/r4d.h:370-371), and repeated launches are
+    bit-identical."""
     banner("row-identity")
     K, N, KB = 2048, 1024, 4
-    words, svh, a, _, _ = _linear_case(K, N, KB, 64, 77)
+    words, svh, a, _, _ = _linear_case(K, N, KB, 16, 77)
     w_d, svh_d = dev(words), dev(svh)
     skg = api.trellis_gemv_skg(K, N, KB)
     full = {}
-    for M in (1, 2, 4, 8, 16, 17, 33, 64):
+    for M in (1, 2, 3, 4, 8, 13, 16):
         full[M] = host_u16(api.trellis_gemm_m64(dev(a[:M]), w_d, svh_d, K, N, KB, skg=skg, out_scale=0.5))
     torch.cuda.synchronize()
     for M, c in full.items():
-        assert np.array_equal(c, full[64][:M]), M
+        assert np.array_equal(c, full[16][:M]), M
     again = host_u16(api.trellis_gemm_m64(dev(a[:8]), w_d, svh_d, K, N, KB, skg=skg, out_scale=0.5))
     assert np.array_equal(again, full[8])
 
