@@ -34,6 +34,7 @@ def parse():
     ap.add_argument("--copies", type=int, default=0, help="weight copies (0: enough for > 1 GiB)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-only", action="store_true", help="only the GEMV launches (for rocprof)")
+    ap.add_argument("--no-m256", action="store_true", help="skip the M = 256 prefill GEMM leg")
     return ap.parse_args()
 
 
@@ -136,6 +137,8 @@ def main():
         per_shape[L["name"]] = {"us": round(avg_ms * 1e3, 2), "GBs": round(ab / (avg_ms * 1e-3) / 1e9, 1)}
     achieved = alg_bytes / (gemv_ms * 1e-3) / 1e9
 
+    m256 = None if args.no_m256 else bench_m256(api, WL, KB)
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(KB)
@@ -163,9 +166,66 @@ def main():
                      "kernel": "tq_gemv_kernel", "avg_launch_us": round(gemv_ms * 1e3 / len(lin), 3),
                      "per_shape_GBs": per_shape},
         "cpu_baseline": cpu,
+        "m256": m256,
         "wall_s": round(wall, 3),
     }
     print(json.dumps(line), flush=True)
+
+
+def bench_m256(api, WL, KB, R=3):
+    """the M = 256 prefill trellis GEMM over the ten projections, fp16 MFMA with fp32
+    accumulate, bf16 out; TFLOP/s = 2 * 256 * K * N per launch over the launch's average duration
+    (back-to-back launches over rotating weight copies in a HIP graph, HIP events on its stream)."""
+    import numpy as np
+    import torch
+    dev = torch.device("cuda:0")
+    M = 256
+    per_shape, tot_flop, tot_ms = {}, 0.0, 0.0
+    for i, (name, K, N) in enumerate(WL.LAYER_SHAPES):
+        nw = K * N * KB // 32
+        copies = max(2, int(np.ceil(1.0e9 / (nw * 4))))
+        words = [torch.randint(-2**31, 2**31 - 1, (nw,), dtype=torch.int32, device=dev) for _ in range(copies)]
+        a = torch.from_numpy(WL.activations_f16(M, K, 40 + i, outlier_frac=0.01)).to(dev)
+        svh = torch.from_numpy(WL.svh_scales(N, 50 + i)).to(dev)
+        skg = api.trellis_m256_skg(K, N, KB)
+        ws = torch.empty(max(1, skg * M * N), dtype=torch.float32, device=dev)
+        tk = api.TicketBuffer(N, dev).t
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+        def run():
+            for c in range(copies):
+                api.trellis_gemm_m256(a, words[c], svh, K, N, KB, skg=skg, out=out, ws=ws, tickets=tk,
+                                      out_scale=0.08838834764831845)
+        run()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                for _ in range(R):
+                    run()
+        torch.cuda.synchronize()
+        g.replay()
+        st = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / (R * copies)
+        flop = 2.0 * M * K * N
+        per_shape[name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(flop / (ms * 1e-3) / 1e12, 1), "skg": skg}
+        tot_flop += flop
+        tot_ms += ms
+        del words
+        torch.cuda.empty_cache()
+    achieved = tot_flop / (tot_ms * 1e-3) / 1e12
+    return {"metric": "M=256 trellis GEMM TFLOP/s (27B layer shapes, KB4)", "value": round(achieved, 1),
+            "unit": "TFLOP/s", "roofline": {"bound": "mfma", "achieved": round(achieved, 1),
+                                            "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                            "frac": round(achieved / FP16_PEAK_TFLOPS, 4)},
+            "kernel": "tq_m256_kernel", "per_shape": per_shape}
 
 
 def cpu_baseline(KB):

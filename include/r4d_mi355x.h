@@ -46,6 +46,26 @@ const char* r4d_gemm_trellis_nt_m64_check(int M, int K, int N, int n_split, int 
  * a shape, the same for every M. */
 int    r4d_mi355x_trellis_gemv_skg(int K, int N, int KB);
 
+/* ---- trellis prefill GEMM, M = 128 or 256 ------------------------------------------------------ */
+/* r4d.h:416-419 r4d_gemm_trellis_nt_m256: the linear of r4d_gemm_trellis_nt_m64 for 128 or 256 rows
+ * (two launches when SKG > 1: the slices, then their sum and the epilogue); ws fp32 ws_bytes(M, N,
+ * SKG) required when SKG > 1 (the reference always requires it); tickets accepted and unused;
+ * (K/16) must be divisible by 4 SKG. SK, NP, U, skw accepted and unused. */
+void r4d_gemm_trellis_nt_m256(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
+                              int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SK, int NP,
+                              int SKG, int U, float out_scale, int64_t stream, int skw);
+/* r4d.h:420-421: NULL when the launch is legal, else the first rule it breaks. */
+const char* r4d_gemm_trellis_nt_m256_check(int M, int K, int N, int n_split, int KB, int SK, int NP,
+                                           int SKG, int U, int skw);
+size_t r4d_gemm_trellis_nt_m256_ws_bytes(int M, int N, int SKG);   /* r4d.h:423 */
+/* No reference counterpart (the m256 test entry of this build, like r4d_gemm_trellis_nt_m64_raw):
+ * fp32 C = A @ Q with no output transform. */
+void r4d_gemm_trellis_nt_m256_raw(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t c, int64_t ws,
+                                  int64_t tickets, int M, int K, int N, int KB, int SKG, int64_t stream);
+/* No reference counterpart (the reference plans with PlanTrellisM256, src/model/linear.cpp:680-724):
+ * this build's SKG for a prefill shape. */
+int r4d_mi355x_trellis_m256_skg(int K, int N, int KB);
+
 /* ---- input transform and FWHT (src/kernels/include/r4dx/kernels/kernels.h) --------------------- */
 /* kernels.h:110-128 r4dx_trellis_input_bf16: out[o][m,k] = f16(FWHT128(fp32(x) * suh[o])[k] * scale),
  * scale = float(2^prescale_log2 / sqrt(128)); x bf16 [M][K]; suh / out: HOST arrays of nout device

@@ -57,6 +57,37 @@ def trellis_gemm_m64(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out=
     return out
 
 
+def trellis_m256_skg(K, N, KB):
+    return lib().r4d_mi355x_trellis_m256_skg(K, N, KB)
+
+
+def trellis_gemm_m256(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out=None, ws=None,
+                      tickets=None, out_scale=1.0, raw=False, stream=None):
+    """C = r4d_gemm_trellis_nt_m256 (bf16 [M][N], M = 128 or 256) or, raw=True, fp32 A @ Q."""
+    L = lib()
+    M = a0.shape[0]
+    skg = trellis_m256_skg(K, N, KB) if skg is None else skg
+    n_split = N if n_split is None else n_split
+    msg = L.r4d_gemm_trellis_nt_m256_check(M, K, N, n_split, KB, 0, 0, skg, 0, 0)
+    if msg:
+        raise ValueError(msg.decode())
+    if ws is None and skg > 1:
+        ws = torch.empty(L.r4d_gemm_trellis_nt_m256_ws_bytes(M, N, skg) // 4, dtype=torch.float32,
+                         device=a0.device)
+    if tickets is None and skg > 1:
+        tickets = TicketBuffer(N, a0.device).t
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32 if raw else torch.bfloat16, device=a0.device)
+    st = _stream(stream)
+    if raw:
+        L.r4d_gemm_trellis_nt_m256_raw(_p(a0), _p(a1), n_split, _p(w), _p(out), _p(ws), _p(tickets),
+                                       M, K, N, KB, skg, st)
+    else:
+        L.r4d_gemm_trellis_nt_m256(_p(a0), _p(a1), n_split, _p(w), _p(svh), _p(out), _p(ws), _p(tickets),
+                                   M, K, N, KB, 0, 0, skg, 0, float(out_scale), st, 0)
+    return out
+
+
 def trellis_reconstruct(w, K, N, KB, stream=None):
     q = torch.empty((K, N), dtype=torch.int16, device=w.device)
     lib().r4d_trellis_reconstruct_f16(_p(w), _p(q), K, N, KB, _stream(stream))

@@ -22,6 +22,11 @@ SIGS = {
     "r4d_trellis_reconstruct_f16": (None, [I64, I64, I32, I32, I32, I64]),
     "r4d_gemm_trellis_nt_m64_check": (CSTR, [I32] * 9),
     "r4d_mi355x_trellis_gemv_skg": (I32, [I32, I32, I32]),
+    "r4d_gemm_trellis_nt_m256": (None, [I64, I64, I32, I64, I64, I64, I64, I64] + [I32] * 8 + [F32, I64, I32]),
+    "r4d_gemm_trellis_nt_m256_check": (CSTR, [I32] * 10),
+    "r4d_gemm_trellis_nt_m256_ws_bytes": (SZ, [I32, I32, I32]),
+    "r4d_gemm_trellis_nt_m256_raw": (None, [I64, I64, I32, I64, I64, I64, I64] + [I32] * 5 + [I64]),
+    "r4d_mi355x_trellis_m256_skg": (I32, [I32, I32, I32]),
     "r4dx_trellis_input_bf16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
     "r4dx_trellis_input_f16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
     "r4dx_fwht128_f32": (None, [I64, I64, I32, I64]),

@@ -44,3 +44,15 @@ def test_sizes_and_rates(L):
 def test_gemv_split_plan(L, K, N):
     skg = L.r4d_mi355x_trellis_gemv_skg(K, N, 4)
     assert skg >= 1 and (K // 16) % skg == 0 and (K // 16) // skg >= 8
+
+
+def test_m256_checks(L):
+    ck = L.r4d_gemm_trellis_nt_m256_check
+    assert ck(256, 5120, 17408, 17408, 4, 0, 0, 4, 0, 0) is None
+    assert ck(128, 5120, 5120, 5120, 5, 0, 0, 1, 0, 0) is None
+    assert b"M must be" in ck(64, 5120, 5120, 5120, 4, 0, 0, 1, 0, 0)
+    assert b"SKG" in ck(256, 5120, 5120, 5120, 4, 0, 0, 3, 0, 0)
+    assert L.r4d_gemm_trellis_nt_m256_ws_bytes(256, 5120, 2) == 2 * 256 * 5120 * 4
+    for K, N in [(5120, 17408), (17408, 5120), (5120, 1024), (6144, 5120)]:
+        skg = L.r4d_mi355x_trellis_m256_skg(K, N, 4)
+        assert ck(256, K, N, N, 4, 0, 0, skg, 0, 0) is None

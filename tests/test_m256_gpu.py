@@ -1,0 +1,88 @@
+"""GPU parity of the M = 256 / 128 prefill trellis GEMM (r4d_gemm_trellis_nt_m256 and its _raw entry)
+through the C ABI.  A f16 ~N(0,1) with 1% of columns x20 (outlier channels).
+
+Bars: fp32 sums within 1e-3 relative error with a 1e-4 * rms(row) floor of the fp64 matmul over the
+oracle-decoded weights; the bf16 linear bit-exact against the oracle's epilogue applied to the
+kernel's own fp32 sums."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from r4dx_amd import workloads as WL
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():
+    pytest.skip("no GPU", allow_module_level=True)
+
+from r4dx_amd import api  # noqa: E402
+from gpu_util import banner, close_rel, dev, host_u16  # noqa: E402
+
+
+def _ref_f64(a_bits, q_bits):
+    a = O.f16_bits_to_f32(a_bits).astype(np.float64)
+    q = O.f16_bits_to_f32(q_bits).astype(np.float64)
+    return a @ q
+
+
+@pytest.mark.parametrize("KB,K,N,M,skg", [
+    (4, 512, 256, 256, 1), (4, 1024, 512, 256, 2), (5, 768, 384, 128, 3), (3, 512, 256, 256, 2),
+    (4, 2048, 128, 256, 8), (5, 1024, 1024, 256, None),
+])
+def test_m256_raw_full(KB, K, N, M, skg):
+    banner("m256", KB, K, N, M, skg)
+    skg = api.trellis_m256_skg(K, N, KB) if skg is None else skg
+    words, suh, svh = WL.trellis_linear(K, N, KB, 7 * K + N)
+    a = WL.activations_f16(M, K, 3, outlier_frac=0.01).view(np.uint16)
+    w_d, a_d = dev(words), dev(a)
+    raw = api.trellis_gemm_m256(a_d, w_d, None, K, N, KB, skg=skg, raw=True)
+    out_scale = np.float32(1.0 / np.sqrt(128.0))
+    full = api.trellis_gemm_m256(a_d, w_d, dev(svh), K, N, KB, skg=skg, out_scale=out_scale)
+    torch.cuda.synchronize()
+    q = O.decode_pair_grid(words, K, N, KB)
+    ref = O.raw_sums(a, q)
+    raw_h = raw.cpu().numpy()
+    assert close_rel(raw_h, ref, 1e-3, 1e-4) <= 1.0
+    assert np.array_equal(host_u16(full), O.epilogue_from_raw(raw_h, svh, out_scale))
+
+
+def test_m256_two_part():
+    banner("m256 two-part")
+    K, N, KB, M = 512, 512, 4, 256
+    words = WL.trellis_words(K, N, KB, 3)
+    a0 = WL.activations_f16(M, K, 4).view(np.uint16)
+    a1 = WL.activations_f16(M, K, 5).view(np.uint16)
+    raw = api.trellis_gemm_m256(dev(a0), dev(words), None, K, N, KB, skg=2, a1=dev(a1), n_split=256, raw=True)
+    torch.cuda.synchronize()
+    q = O.decode_pair_grid(words, K, N, KB)
+    ref = O.raw_sums(a0, q, a1=a1, n_split=256)
+    assert close_rel(raw.cpu().numpy(), ref, 1e-3, 1e-4) <= 1.0
+
+
+def test_m256_rows_independent():
+    """A row's bits do not depend on the other rows: permuting A's rows permutes C's rows."""
+    banner("m256 rows")
+    K, N, KB, M = 1024, 256, 4, 256
+    words, suh, svh = WL.trellis_linear(K, N, KB, 9)
+    a = WL.activations_f16(M, K, 10).view(np.uint16)
+    perm = np.random.default_rng(0).permutation(M)
+    w_d = dev(words)
+    c1 = host_u16(api.trellis_gemm_m256(dev(a), w_d, dev(svh), K, N, KB, skg=2, out_scale=0.25))
+    c2 = host_u16(api.trellis_gemm_m256(dev(a[perm]), w_d, dev(svh), K, N, KB, skg=2, out_scale=0.25))
+    torch.cuda.synchronize()
+    assert np.array_equal(c1[perm], c2)
+
+
+@pytest.mark.parametrize("name,K,N", WL.LAYER_SHAPES)
+def test_config2_shapes(name, K, N):
+    """every projection at M = 256, KB 4 (and KB 5 on the MLP), against the fp64
+    matmul over the oracle-decoded weights."""
+    for KB in ((4, 5) if name.startswith("mlp") else (4,)):
+        banner("config2", name, K, N, KB)
+        words = WL.trellis_words(K, N, KB, hash(name) % 997)
+        a = WL.activations_f16(256, K, 11, outlier_frac=0.01).view(np.uint16)
+        raw = api.trellis_gemm_m256(dev(a), dev(words), None, K, N, KB, raw=True)
+        torch.cuda.synchronize()
+        q = O.decode_pair_grid(words, K, N, KB)
+        ref = _ref_f64(a, q)
+        assert close_rel(raw.cpu().numpy(), ref, 1e-3, 1e-4) <= 1.0, KB
