@@ -35,6 +35,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-only", action="store_true", help="only the GEMV launches (for rocprof)")
     ap.add_argument("--no-m256", action="store_true", help="skip the M = 256 prefill GEMM leg")
+    ap.add_argument("--no-w4", action="store_true", help="skip the w4a16 LM-head leg")
     return ap.parse_args()
 
 
@@ -138,6 +139,7 @@ def main():
     achieved = alg_bytes / (gemv_ms * 1e-3) / 1e9
 
     m256 = None if args.no_m256 else bench_m256(api, WL, KB)
+    w4 = None if args.no_w4 else bench_w4a16(api, WL)
 
     cpu = None
     if not args.no_cpu:
@@ -167,6 +169,7 @@ def main():
                      "per_shape_GBs": per_shape},
         "cpu_baseline": cpu,
         "m256": m256,
+        "w4a16": w4,
         "wall_s": round(wall, 3),
     }
     print(json.dumps(line), flush=True)
@@ -226,6 +229,61 @@ def bench_m256(api, WL, KB, R=3):
                                             "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                             "frac": round(achieved / FP16_PEAK_TFLOPS, 4)},
             "kernel": "tq_m256_kernel", "per_shape": per_shape}
+
+
+def bench_w4a16(api, WL, R=4):
+    """the w4a16 LM head (N = 248 320, K = 5120) at groups 32 / 64 and M = 1 / 8, fp32
+    logits + per-row argmax. GB/s = (N K / 2 + N K / g * 4) bytes over the GEMM's average launch time
+    (back-to-back in a HIP graph over 2 weight copies, > the 256 MB MALL)."""
+    import torch
+    dev = torch.device("cuda:0")
+    N, K = 248320, 5120
+    res = {}
+    for g in (32, 64):
+        copies = []
+        for cidx in range(2):
+            wq, wsz = WL.w4a16_packed(N, K, g, 100 + cidx)
+            copies.append((torch.from_numpy(wq.view("int32")).to(dev), torch.from_numpy(wsz.view("int32")).to(dev)))
+        for M in (1, 8):
+            a = torch.from_numpy(WL.activations_f16(M, K, 5)).to(dev)
+            out = torch.empty((M, N), dtype=torch.float32, device=dev)
+            idx = torch.empty(M, dtype=torch.int32, device=dev)
+            val = torch.empty(M, dtype=torch.float32, device=dev)
+
+            def run(with_argmax):
+                for wq_d, wsz_d in copies:
+                    api.w4a16_gemm(a, wq_d, wsz_d, K, N, g, out=out, f32=True)
+                    if with_argmax:
+                        api.argmax_rows(out, idx, val)
+            times = {}
+            for with_am in (False, True):
+                run(with_am)
+                torch.cuda.synchronize()
+                gr = torch.cuda.CUDAGraph()
+                s = torch.cuda.Stream()
+                s.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(s):
+                    with torch.cuda.graph(gr, stream=s):
+                        for _ in range(R):
+                            run(with_am)
+                torch.cuda.synchronize()
+                gr.replay()
+                st = torch.cuda.current_stream()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(st)
+                gr.replay()
+                e1.record(st)
+                torch.cuda.synchronize()
+                times[with_am] = e0.elapsed_time(e1) / (R * len(copies))
+            nbytes = N * K / 2 + N * K / g * 4
+            res[f"g{g}_M{M}"] = {"gemm_us": round(times[False] * 1e3, 2),
+                                 "GBs": round(nbytes / (times[False] * 1e-3) / 1e9, 1),
+                                 "frac": round(nbytes / (times[False] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                 "gemm_plus_argmax_us": round(times[True] * 1e3, 2)}
+        del copies
+        torch.cuda.empty_cache()
+    return {"metric": "w4a16 LM head (N=248320, K=5120) effective HBM GB/s", "kernel": "w4_kernel",
+            "peak_GBs": HBM_PEAK_GBS, "cases": res}
 
 
 def cpu_baseline(KB):

@@ -66,6 +66,41 @@ void r4d_gemm_trellis_nt_m256_raw(int64_t a0, int64_t a1, int n_split, int64_t w
  * this build's SKG for a prefill shape. */
 int r4d_mi355x_trellis_m256_skg(int K, int N, int KB);
 
+/* ---- w4a16 group-quantized skinny GEMM (LM head, drafters) ------------------------------------- */
+/* r4d.h:331-333: C bf16 [M][N] = A f16 [M][K] @ dequant(Wq, Wsz)^T at the build-default group 64; Wq in
+ * the packed fragment order of quant_int4.hpp:171-198, Wsz (tile, group, row) dwords = f16 scale | f16
+ * (-(1024 + zero)) << 16. WV, SK, MB, NPW, NT accepted and unused. M 1..64 (M x K bounded by the LDS
+ * copy of A: M <= 8 at K = 5120), N % 16 == 0, K % 64 == 0. */
+void r4d_gemm_w4a16_nt_m64(int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int N, int WV, int SK,
+                           int MB, int NPW, int NT, int64_t stream);
+int  r4d_gemm_w4a16_nt_m64_max_m(void);            /* r4d.h:333 */
+int  r4d_gemm_w4a16_nt_m64_group(void);            /* r4d.h:334 */
+int  r4d_gemm_w4a16_nt_m64_has_group(int group);   /* r4d.h:340: 1 for 32 and 64 */
+/* r4d.h:341-342: the same at a per-call group (32 or 64). */
+void r4d_gemm_w4a16_nt_m64_g(int group, int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int N, int WV,
+                             int SK, int MB, int NPW, int NT, int64_t stream);
+/* No reference counterpart: the legality rules of the two entries above without launching. */
+const char* r4d_gemm_w4a16_nt_m64_check(int group, int M, int K, int N);
+/* No reference counterpart (BASELINE config 3 asks for fp32 logits; the reference C is bf16): the
+ * same GEMM with fp32 C [M][N]. */
+void r4d_gemm_w4a16_nt_m64_f32(int group, int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int N,
+                               int64_t stream);
+
+/* ---- argmax (src/kernels/include/r4dx/kernels/kernels.h:297-330) -------------------------------- */
+/* out_idx[0] = argmax over logits[0, vocab): larger value first, then lower index; a NaN never wins,
+ * a row with nothing above -inf gives index 0 (argmax_ref.hpp:22-41). Two launches over a
+ * library-owned per-device partial buffer: calls that overlap on one device race. */
+void r4dx_argmax_f32(int64_t logits, int64_t out_idx, int64_t vocab, int64_t stream);          /* :308 */
+void r4dx_argmax_val_f32(int64_t logits, int64_t out_idx, int64_t out_val, int64_t vocab,
+                         int64_t stream);                                                       /* :316 */
+void r4dx_argmax_bf16(int64_t logits, int64_t out_idx, int64_t vocab, int64_t stream);         /* :320 */
+void r4dx_argmax_val_bf16(int64_t logits, int64_t out_idx, int64_t out_val, int64_t vocab,
+                          int64_t stream);                                                      /* :321 */
+/* kernels.h:328-329: rows (at most 64 here, 16 in the reference) of a [rows][row_stride] logits array;
+ * row r's result at out_idx[r * out_stride] (and out_val[r * out_stride] when out_val != 0). */
+void r4dx_argmax_rows_f32(int64_t logits, int64_t row_stride, int64_t out_idx, int64_t out_val,
+                          int64_t out_stride, int64_t rows, int64_t vocab, int64_t stream);
+
 /* ---- input transform and FWHT (src/kernels/include/r4dx/kernels/kernels.h) --------------------- */
 /* kernels.h:110-128 r4dx_trellis_input_bf16: out[o][m,k] = f16(FWHT128(fp32(x) * suh[o])[k] * scale),
  * scale = float(2^prescale_log2 / sqrt(128)); x bf16 [M][K]; suh / out: HOST arrays of nout device

@@ -111,3 +111,38 @@ def trellis_input(x, suh_list, prescale=0, bf16=True, outs=None, stream=None):
 def fwht128(x, stream=None):
     lib().r4dx_fwht128_f32(_p(x), x.numel() // 128, 0, _stream(stream))
     return x
+
+
+def w4a16_gemm(a, wq, wsz, K, N, group=64, out=None, f32=False, stream=None):
+    """C = r4d_gemm_w4a16_nt_m64_g (bf16) or, f32=True, r4d_gemm_w4a16_nt_m64_f32 (fp32 logits)."""
+    L = lib()
+    M = a.shape[0]
+    msg = L.r4d_gemm_w4a16_nt_m64_check(group, M, K, N)
+    if msg:
+        raise ValueError(msg.decode())
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32 if f32 else torch.bfloat16, device=a.device)
+    st = _stream(stream)
+    if f32:
+        L.r4d_gemm_w4a16_nt_m64_f32(group, _p(a), _p(wq), _p(wsz), _p(out), M, K, N, st)
+    else:
+        L.r4d_gemm_w4a16_nt_m64_g(group, _p(a), _p(wq), _p(wsz), _p(out), M, K, N, 0, 0, 0, 0, 0, st)
+    return out
+
+
+def argmax_rows(logits, out_idx=None, out_val=None, stream=None):
+    """Per-row argmax of a [rows][vocab] fp32 or bf16 tensor: (int32 [rows], fp32 [rows])."""
+    L = lib()
+    rows, vocab = logits.shape
+    if out_idx is None:
+        out_idx = torch.empty(rows, dtype=torch.int32, device=logits.device)
+    if out_val is None:
+        out_val = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    st = _stream(stream)
+    if logits.dtype == torch.float32:
+        L.r4dx_argmax_rows_f32(_p(logits), logits.stride(0), _p(out_idx), _p(out_val), 1, rows, vocab, st)
+    elif logits.dtype == torch.bfloat16 and rows == 1:
+        L.r4dx_argmax_val_bf16(_p(logits), _p(out_idx), _p(out_val), vocab, st)
+    else:
+        raise ValueError("fp32 rows or a single bf16 row")
+    return out_idx, out_val

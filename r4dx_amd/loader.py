@@ -27,6 +27,18 @@ SIGS = {
     "r4d_gemm_trellis_nt_m256_ws_bytes": (SZ, [I32, I32, I32]),
     "r4d_gemm_trellis_nt_m256_raw": (None, [I64, I64, I32, I64, I64, I64, I64] + [I32] * 5 + [I64]),
     "r4d_mi355x_trellis_m256_skg": (I32, [I32, I32, I32]),
+    "r4d_gemm_w4a16_nt_m64": (None, [I64, I64, I64, I64] + [I32] * 8 + [I64]),
+    "r4d_gemm_w4a16_nt_m64_max_m": (I32, []),
+    "r4d_gemm_w4a16_nt_m64_group": (I32, []),
+    "r4d_gemm_w4a16_nt_m64_has_group": (I32, [I32]),
+    "r4d_gemm_w4a16_nt_m64_g": (None, [I32, I64, I64, I64, I64] + [I32] * 8 + [I64]),
+    "r4d_gemm_w4a16_nt_m64_check": (CSTR, [I32] * 4),
+    "r4d_gemm_w4a16_nt_m64_f32": (None, [I32, I64, I64, I64, I64, I32, I32, I32, I64]),
+    "r4dx_argmax_f32": (None, [I64, I64, I64, I64]),
+    "r4dx_argmax_val_f32": (None, [I64, I64, I64, I64, I64]),
+    "r4dx_argmax_bf16": (None, [I64, I64, I64, I64]),
+    "r4dx_argmax_val_bf16": (None, [I64, I64, I64, I64, I64]),
+    "r4dx_argmax_rows_f32": (None, [I64] * 8),
     "r4dx_trellis_input_bf16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
     "r4dx_trellis_input_f16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
     "r4dx_fwht128_f32": (None, [I64, I64, I32, I64]),

@@ -47,3 +47,17 @@ def activations_f16(M, K, seed, outlier_frac=0.0, outlier_scale=20.0):
 def trellis_linear(K, N, KB, seed):
     """(words, suh, svh) of one trellis linear."""
     return trellis_words(K, N, KB, seed), signs(K, seed + 1), svh_scales(N, seed + 2)
+
+
+def w4a16_packed(N, K, group, seed):
+    """BASELINE config 3's weights directly in the packed form: uniform random nibbles, per (row, group)
+    an fp16 scale ~ lognormal around 0.02 and an int4 zero point uniform in 0..15.
+    Returns (wq uint32 [N*K/8], wsz uint32 [N/16][K/group][16])."""
+    rng = np.random.default_rng(seed)
+    wq = rng.integers(0, 2**32, N * K // 8, dtype=np.uint64).astype(np.uint32)
+    gpr = K // group
+    sc = rng.lognormal(np.log(0.02), 0.3, (N // 16, gpr, 16)).astype(np.float16).view(np.uint16)
+    zero = rng.integers(0, 16, (N // 16, gpr, 16))
+    nz = (-(1024.0 + zero)).astype(np.float16).view(np.uint16)
+    wsz = (sc.astype(np.uint32) | (nz.astype(np.uint32) << 16)).reshape(-1)
+    return wq, wsz

@@ -56,3 +56,13 @@ def test_m256_checks(L):
     for K, N in [(5120, 17408), (17408, 5120), (5120, 1024), (6144, 5120)]:
         skg = L.r4d_mi355x_trellis_m256_skg(K, N, 4)
         assert ck(256, K, N, N, 4, 0, 0, skg, 0, 0) is None
+
+
+def test_w4a16_checks(L):
+    ck = L.r4d_gemm_w4a16_nt_m64_check
+    assert ck(32, 1, 5120, 248320) is None and ck(64, 8, 5120, 248320) is None
+    assert b"group" in ck(128, 1, 5120, 248320)
+    assert b"N must" in ck(64, 1, 5120, 248321)
+    assert b"K must" in ck(64, 1, 5100, 256)
+    assert [L.r4d_gemm_w4a16_nt_m64_has_group(g) for g in (16, 32, 64, 128)] == [0, 1, 1, 0]
+    assert L.r4d_gemm_w4a16_nt_m64_group() == 64 and L.r4d_gemm_w4a16_nt_m64_max_m() == 64
