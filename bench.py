@@ -36,6 +36,7 @@ def parse():
     ap.add_argument("--kernel-only", action="store_true", help="only the GEMV launches (for rocprof)")
     ap.add_argument("--no-m256", action="store_true", help="skip the M = 256 prefill GEMM leg")
     ap.add_argument("--no-w4", action="store_true", help="skip the w4a16 LM-head leg")
+    ap.add_argument("--no-i8", action="store_true", help="skip the int8 prefill GEMM leg")
     return ap.parse_args()
 
 
@@ -140,6 +141,7 @@ def main():
 
     m256 = None if args.no_m256 else bench_m256(api, WL, KB)
     w4 = None if args.no_w4 else bench_w4a16(api, WL)
+    i8 = None if args.no_i8 else bench_int8(api, WL)
 
     cpu = None
     if not args.no_cpu:
@@ -170,6 +172,7 @@ def main():
         "cpu_baseline": cpu,
         "m256": m256,
         "w4a16": w4,
+        "int8": i8,
         "wall_s": round(wall, 3),
     }
     print(json.dumps(line), flush=True)
@@ -284,6 +287,70 @@ def bench_w4a16(api, WL, R=4):
         torch.cuda.empty_cache()
     return {"metric": "w4a16 LM head (N=248320, K=5120) effective HBM GB/s", "kernel": "w4_kernel",
             "peak_GBs": HBM_PEAK_GBS, "cases": res}
+
+
+def _graph_ms(fn, R, per):
+    """Average ms of one of `per` launches inside fn, replayed R times in a HIP graph (events on the
+    graph's launch stream)."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(R):
+                fn()
+    torch.cuda.synchronize()
+    g.replay()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    g.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (R * per)
+
+
+def bench_int8(api, WL, R=4):
+    """the int8 x int8 prefill GEMM at M = 256, (K, N) = (5120, 17408) and (17408, 5120),
+    fp32 column weight scales, row (and per-128) activation scales. TOP/s = 2 M K N over the GEMM's average
+    launch time; the roofline is the larger of the int8 MFMA time (5.0 POP/s) and the HBM time of the
+    algorithmic bytes (N K weight bytes + M K + 2 M N + 4 N); the quantizer is timed beside it."""
+    import torch
+    dev = torch.device("cuda:0")
+    M = 256
+    res = {}
+    for K, N in ((5120, 17408), (17408, 5120)):
+        x, w8, sw = WL.int8_case(K, N, 3)
+        copies = 12
+        ws_ = [torch.from_numpy(w8).to(dev) for _ in range(copies)]
+        sw_d = torch.from_numpy(sw).to(dev)
+        x_d = torch.from_numpy(x.view("int16")).to(dev)
+        skg = api.i8_dense_skg(K, N)
+        for blk in (False, True):
+            a8, sa = api.i8_quant(x_d, blk)
+            out = torch.empty((M, N), dtype=torch.float16, device=dev)
+            wsb = torch.empty(max(1, api.lib().r4d_gemm_i8_dense_ws_bytes(M, N, skg) // 4), dtype=torch.int32,
+                              device=dev)
+
+            def gemm():
+                for w_d in ws_:
+                    api.i8_dense_gemm(a8, sa, w_d, sw_d, K, N, scale_blk=blk, skg=skg, out=out, ws=wsb)
+            ms = _graph_ms(gemm, R, copies)
+            qms = _graph_ms(lambda: [api.i8_quant(x_d, blk) for _ in range(4)], R, 4)
+            ops = 2.0 * M * K * N
+            nbytes = N * K + M * K + 2 * M * N + 4 * N
+            floor_ms = max(ops / 5.0e15, nbytes / (HBM_PEAK_GBS * 1e9)) * 1e3
+            res[f"K{K}_N{N}_{'blk' if blk else 'row'}"] = {
+                "gemm_us": round(ms * 1e3, 2), "TOPs": round(ops / (ms * 1e-3) / 1e12, 1),
+                "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1), "roofline_frac": round(floor_ms / ms, 4),
+                "quant_us": round(qms * 1e3, 2), "skg": skg}
+        del ws_
+        torch.cuda.empty_cache()
+    return {"metric": "int8 x int8 prefill GEMM TOP/s (M=256)", "kernel": "i8_dense_kernel",
+            "peak_TOPs": 5000.0, "peak_GBs": HBM_PEAK_GBS, "cases": res}
 
 
 def cpu_baseline(KB):

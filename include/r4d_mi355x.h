@@ -101,6 +101,32 @@ void r4dx_argmax_val_bf16(int64_t logits, int64_t out_idx, int64_t out_val, int6
 void r4dx_argmax_rows_f32(int64_t logits, int64_t row_stride, int64_t out_idx, int64_t out_val,
                           int64_t out_stride, int64_t rows, int64_t vocab, int64_t stream);
 
+/* ---- int8 x int8 prefill GEMM and its activation quantizers ------------------------------------ */
+/* r4d.h:490-491 r4d_trellis_i8_quant_act: x f16 [256][K] (part p at x + p part_stride elements) -> the A8
+ * fragment layout (r4d_trellis_i8_layout.h:32-45) at a8 + p 256 K bytes, SA [K/128][256] per part at
+ * sa + p (K/128) 256 floats; s = amax / 127 per (row, 128 k) (1 for all zero), q = clamp(rint(x / s)). */
+void r4d_trellis_i8_quant_act(int64_t x, int64_t a8, int64_t sa, int parts, int64_t part_stride, int K,
+                              int64_t stream);
+/* r4d.h:517-518 r4d_trellis_i8_quant_act_row: the same with one scale per row, SA [256] per part. */
+void r4d_trellis_i8_quant_act_row(int64_t x, int64_t a8, int64_t sa, int parts, int64_t part_stride, int K,
+                                  int64_t stream);
+/* No reference counterpart (the dense GEMM's operand): a8 plain [M][K]; blk != 0: sa [K/128][M], else
+ * sa [M]. */
+void r4d_i8_quant_act_plain(int64_t x, int64_t a8, int64_t sa, int M, int K, int blk, int64_t stream);
+/* No reference counterpart as an entry (the reference's dense int8 GEMM is the bench-only
+ * i8g_kernel<TRELLIS = false>, r4d_trellis_i8.h:19-20): C f16 [256][N] = scales x int32(A8 . W8^T),
+ * a8 plain [256][K], w8 plain [N][K], sw fp32 [N]; scale_blk: sa [K/128][256] (per-128 activation
+ * scales, r4d_trellis_i8.h:36 RESC 3 math) else sa [256] (row scales). ws ws_bytes(M, N, SKG) when
+ * SKG > 1 (then two launches). */
+void r4d_gemm_i8_dense(int64_t a8, int64_t sa, int64_t w8, int64_t sw, int64_t c, int64_t ws, int M, int K, int N,
+                       int SKG, int scale_blk, int64_t stream);
+/* Test entry: the exact int32 sums [256][N] of the same kernel (always two launches; ws required). */
+void r4d_gemm_i8_dense_raw(int64_t a8, int64_t w8, int64_t c, int64_t ws, int M, int K, int N, int SKG,
+                           int64_t stream);
+const char* r4d_gemm_i8_dense_check(int M, int K, int N, int SKG);
+size_t r4d_gemm_i8_dense_ws_bytes(int M, int N, int SKG);
+int r4d_mi355x_i8_skg(int K, int N);
+
 /* ---- input transform and FWHT (src/kernels/include/r4dx/kernels/kernels.h) --------------------- */
 /* kernels.h:110-128 r4dx_trellis_input_bf16: out[o][m,k] = f16(FWHT128(fp32(x) * suh[o])[k] * scale),
  * scale = float(2^prescale_log2 / sqrt(128)); x bf16 [M][K]; suh / out: HOST arrays of nout device

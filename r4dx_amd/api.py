@@ -146,3 +146,43 @@ def argmax_rows(logits, out_idx=None, out_val=None, stream=None):
     else:
         raise ValueError("fp32 rows or a single bf16 row")
     return out_idx, out_val
+
+
+def i8_quant(x, blk=False, ref_layout=False, stream=None):
+    """Activation quantizer: x f16 [M][K] -> (a8 int8, sa fp32). ref_layout: the reference A8 fragment
+    layout (M = 256, r4d_trellis_i8_quant_act / _row); else plain [M][K] (r4d_i8_quant_act_plain)."""
+    L = lib()
+    M, K = x.shape
+    a8 = torch.empty(M * K, dtype=torch.int8, device=x.device)
+    sa = torch.empty((K // 128) * M if blk else M, dtype=torch.float32, device=x.device)
+    st = _stream(stream)
+    if ref_layout:
+        f = L.r4d_trellis_i8_quant_act if blk else L.r4d_trellis_i8_quant_act_row
+        f(_p(x), _p(a8), _p(sa), 1, 0, K, st)
+    else:
+        L.r4d_i8_quant_act_plain(_p(x), _p(a8), _p(sa), M, K, int(blk), st)
+    return a8, sa
+
+
+def i8_dense_skg(K, N):
+    return lib().r4d_mi355x_i8_skg(K, N)
+
+
+def i8_dense_gemm(a8, sa, w8, sw, K, N, scale_blk=False, skg=None, raw=False, out=None, ws=None, stream=None):
+    """C f16 [256][N] = r4d_gemm_i8_dense, or raw=True the exact int32 sums (r4d_gemm_i8_dense_raw)."""
+    L = lib()
+    M = 256
+    skg = i8_dense_skg(K, N) if skg is None else skg
+    msg = L.r4d_gemm_i8_dense_check(M, K, N, skg)
+    if msg:
+        raise ValueError(msg.decode())
+    if ws is None and (skg > 1 or raw):
+        ws = torch.empty(L.r4d_gemm_i8_dense_ws_bytes(M, N, skg) // 4, dtype=torch.int32, device=a8.device)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.int32 if raw else torch.float16, device=a8.device)
+    st = _stream(stream)
+    if raw:
+        L.r4d_gemm_i8_dense_raw(_p(a8), _p(w8), _p(out), _p(ws), M, K, N, skg, st)
+    else:
+        L.r4d_gemm_i8_dense(_p(a8), _p(sa), _p(w8), _p(sw), _p(out), _p(ws), M, K, N, skg, int(scale_blk), st)
+    return out

@@ -61,3 +61,13 @@ def w4a16_packed(N, K, group, seed):
     nz = (-(1024.0 + zero)).astype(np.float16).view(np.uint16)
     wsz = (sc.astype(np.uint32) | (nz.astype(np.uint32) << 16)).reshape(-1)
     return wq, wsz
+
+
+def int8_case(K, N, seed, M=256):
+    """activations f16 Student-t (nu = 4); weights int8 uniform in [-127, 127] with an
+    fp32 scale per output column (log-normal around 0.01)."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_t(4, (M, K)).astype(np.float16)
+    w8 = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    sw = rng.lognormal(np.log(0.01), 0.3, N).astype(np.float32)
+    return x, w8, sw
