@@ -315,9 +315,11 @@ def _graph_ms(fn, R, per):
 
 def bench_int8(api, WL, R=4):
     """the int8 x int8 prefill GEMM at M = 256, (K, N) = (5120, 17408) and (17408, 5120),
-    fp32 column weight scales, row (and per-128) activation scales. TOP/s = 2 M K N over the GEMM's average
-    launch time; the roofline is the larger of the int8 MFMA time (5.0 POP/s) and the HBM time of the
-    algorithmic bytes (N K weight bytes + M K + 2 M N + 4 N); the quantizer is timed beside it."""
+    int8 weights (W8 block layout) with an fp32 scale per column, activations quantized per row (scale mode 0)
+    or per (row, 128) (mode 1). TOP/s = 2 M K N over the GEMM's average launch time (12 weight copies back to
+    back in a HIP graph); the roofline floor is the larger of the int8 MFMA time (5.0 POP/s) and the HBM time of
+    the algorithmic bytes (N K weight bytes + M K + 2 M N + 4 N + the activation scales); the activation
+    quantizer is timed beside it."""
     import torch
     dev = torch.device("cuda:0")
     M = 256
@@ -325,31 +327,31 @@ def bench_int8(api, WL, R=4):
     for K, N in ((5120, 17408), (17408, 5120)):
         x, w8, sw = WL.int8_case(K, N, 3)
         copies = 12
-        ws_ = [torch.from_numpy(w8).to(dev) for _ in range(copies)]
+        w_d = api.i8_pack_w(torch.from_numpy(w8).to(dev))
+        ws_ = [w_d] + [w_d.clone() for _ in range(copies - 1)]
         sw_d = torch.from_numpy(sw).to(dev)
         x_d = torch.from_numpy(x.view("int16")).to(dev)
         skg = api.i8_dense_skg(K, N)
-        for blk in (False, True):
-            a8, sa = api.i8_quant(x_d, blk)
+        for mode in (0, 1):
+            a8, sa = api.i8_quant(x_d, mode != 0)
             out = torch.empty((M, N), dtype=torch.float16, device=dev)
-            wsb = torch.empty(max(1, api.lib().r4d_gemm_i8_dense_ws_bytes(M, N, skg) // 4), dtype=torch.int32,
-                              device=dev)
+            work = api.I8Workspace(N, skg, dev)
 
             def gemm():
-                for w_d in ws_:
-                    api.i8_dense_gemm(a8, sa, w_d, sw_d, K, N, scale_blk=blk, skg=skg, out=out, ws=wsb)
+                for w in ws_:
+                    api.i8_dense_gemm(a8, sa, w, sw_d, K, N, scale_mode=mode, skg=skg, out=out, work=work)
             ms = _graph_ms(gemm, R, copies)
-            qms = _graph_ms(lambda: [api.i8_quant(x_d, blk) for _ in range(4)], R, 4)
+            qms = _graph_ms(lambda: [api.i8_quant(x_d, mode != 0) for _ in range(4)], R, 4)
             ops = 2.0 * M * K * N
-            nbytes = N * K + M * K + 2 * M * N + 4 * N
+            nbytes = N * K + M * K + 2 * M * N + 4 * N + 4 * sa.numel()
             floor_ms = max(ops / 5.0e15, nbytes / (HBM_PEAK_GBS * 1e9)) * 1e3
-            res[f"K{K}_N{N}_{'blk' if blk else 'row'}"] = {
+            res[f"K{K}_N{N}_{'blk' if mode else 'row'}"] = {
                 "gemm_us": round(ms * 1e3, 2), "TOPs": round(ops / (ms * 1e-3) / 1e12, 1),
                 "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1), "roofline_frac": round(floor_ms / ms, 4),
                 "quant_us": round(qms * 1e3, 2), "skg": skg}
-        del ws_
+        del ws_, w_d
         torch.cuda.empty_cache()
-    return {"metric": "int8 x int8 prefill GEMM TOP/s (M=256)", "kernel": "i8_dense_kernel",
+    return {"metric": "int8 x int8 prefill GEMM TOP/s (M=256)", "kernel": "i8_gemm_kernel",
             "peak_TOPs": 5000.0, "peak_GBs": HBM_PEAK_GBS, "cases": res}
 
 

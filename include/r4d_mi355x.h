@@ -113,16 +113,20 @@ void r4d_trellis_i8_quant_act_row(int64_t x, int64_t a8, int64_t sa, int parts, 
 /* No reference counterpart (the dense GEMM's operand): a8 plain [M][K]; blk != 0: sa [K/128][M], else
  * sa [M]. */
 void r4d_i8_quant_act_plain(int64_t x, int64_t a8, int64_t sa, int M, int K, int blk, int64_t stream);
-/* No reference counterpart as an entry (the reference's dense int8 GEMM is the bench-only
- * i8g_kernel<TRELLIS = false>, r4d_trellis_i8.h:19-20): C f16 [256][N] = scales x int32(A8 . W8^T),
- * a8 plain [256][K], w8 plain [N][K], sw fp32 [N]; scale_blk: sa [K/128][256] (per-128 activation
- * scales, r4d_trellis_i8.h:36 RESC 3 math) else sa [256] (row scales). ws ws_bytes(M, N, SKG) when
- * SKG > 1 (then two launches). */
-void r4d_gemm_i8_dense(int64_t a8, int64_t sa, int64_t w8, int64_t sw, int64_t c, int64_t ws, int M, int K, int N,
-                       int SKG, int scale_blk, int64_t stream);
-/* Test entry: the exact int32 sums [256][N] of the same kernel (always two launches; ws required). */
-void r4d_gemm_i8_dense_raw(int64_t a8, int64_t w8, int64_t c, int64_t ws, int M, int K, int N, int SKG,
-                           int64_t stream);
+/* No reference counterpart as an entry: the reference has the dense form only as its bench kernel
+ * (i8g_kernel<TRELLIS = false>, r4d_trellis_i8.h:19-21), with the same operand layouts. C f16 [256][N].
+ * a8: A8 layout (r4d_trellis_i8_quant_act / _row); w8: W8 block layout (r4d_trellis_i8_layout.h:24-27,
+ * r4d_i8_pack_w). scale_mode 0: sa [256], sw [N] (one int32 sum per slice, scaled once); 1: sa [K/128][256],
+ * sw [N]; 2: sa [K/128][256], sw [K/128][N] (per 128-k block: acc += float(int32) * scale). SKG > 1 splits K
+ * over the grid: ws r4d_gemm_i8_dense_ws_bytes(M, N, SKG) and tickets u32 [N/128], zero before the first call
+ * and self-resetting (the protocol of r4d.h:482-486). */
+void r4d_gemm_i8_dense(int64_t a8, int64_t sa, int64_t w8, int64_t sw, int64_t c, int64_t ws, int64_t tickets, int M,
+                       int K, int N, int SKG, int scale_mode, int64_t stream);
+/* Test entry: the exact int32 sums [256][N] of the same kernel and split. */
+void r4d_gemm_i8_dense_raw(int64_t a8, int64_t w8, int64_t c, int64_t ws, int64_t tickets, int M, int K, int N,
+                           int SKG, int64_t stream);
+/* Plain int8 [N][K] -> the W8 block layout (r4d_trellis_i8_layout.h:56-64 W8Offset); N % 32 == 0, K % 16 == 0. */
+void r4d_i8_pack_w(int64_t wp, int64_t w8, int N, int K, int64_t stream);
 const char* r4d_gemm_i8_dense_check(int M, int K, int N, int SKG);
 size_t r4d_gemm_i8_dense_ws_bytes(int M, int N, int SKG);
 int r4d_mi355x_i8_skg(int K, int N);

@@ -367,6 +367,22 @@ size_t r4o_a8_offset(int r, int k, int K) {
   return ((((size_t)rg * KT + kt) * 4 + i) * 32 + lane) * 8 + e;
 }
 
+/* r4d_trellis_i8_layout.h:24-27,56-64 W8Offset: the (32-column pair, 16-k tile) block is 512 B; lane L's
+ * 16 B = fragment F0 then F1, element e of F on lane L is column 32 pair + 16 ((L >> 3) & 1) + 8 F + (L & 7)
+ * and k = 16 kt + 8 (e >> 2) + 4 (L >> 4) + (e & 3). */
+size_t r4o_w8_offset(int n, int k, int K) {
+  const int k16 = k & 15;
+  const int h = (k16 >> 2) & 1, e = 4 * (k16 >> 3) + (k16 & 3);
+  const int pair = n >> 5, j = n & 31, t = j >> 4, F = (j >> 3) & 1, c = j & 7;
+  const int lane = 16 * h + 8 * t + c;
+  return ((size_t)pair * (K >> 4) + (k >> 4)) * 512 + (size_t)lane * 16 + F * 8 + e;
+}
+
+void r4o_pack_w8(const int8_t* wp, int N, int K, int8_t* w8) {
+  for (int n = 0; n < N; ++n)
+    for (int k = 0; k < K; ++k) w8[r4o_w8_offset(n, k, K)] = wp[(size_t)n * K + k];
+}
+
 void r4o_pack_a8(const int8_t* ap, int K, int8_t* a8) {
   for (int r = 0; r < 256; ++r)
     for (int k = 0; k < K; ++k) a8[r4o_a8_offset(r, k, K)] = ap[(size_t)r * K + k];

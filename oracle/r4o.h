@@ -88,6 +88,8 @@ void     r4o_i8_gemm_ref(const int8_t* a, const float* sa, const int8_t* w, cons
 /* A8 fragment layout of r4d_trellis_i8_layout.h:32-45 (plain [256][K] -> A8 bytes) */
 size_t   r4o_a8_offset(int r, int k, int K);
 void     r4o_pack_a8(const int8_t* ap, int K, int8_t* a8);
+size_t   r4o_w8_offset(int n, int k, int K);
+void     r4o_pack_w8(const int8_t* wp, int N, int K, int8_t* w8);
 
 /* ---- w4a16 (src/convert/include/r4dx_convert/quant_int4.hpp) ---------------------------------- */
 /* quant_int4.hpp:95-160 QuantizeInt4Asymmetric: w fp32 [N][K] -> q [N][K] 0..15, scale/zero

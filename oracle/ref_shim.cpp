@@ -80,6 +80,7 @@ void ref_i8_gemm(const int8_t* A, const float* sa, const int8_t* W, const float*
   i8p::RefGemmInt8(A, sa, W, sw, M, N, K, mask, C);
 }
 size_t ref_a8_offset(int r, int k, int K) { return i8p::A8Offset(r, k, K); }
+size_t ref_w8_offset(int n, int k, int K) { return i8p::W8Offset(n, k, K); }
 int8_t ref_i8_quant_w(uint16_t w, uint16_t rs) { return i8p::QuantWTrick(w, rs); }
 uint16_t ref_i8_rs_half(float s) { return i8p::RsHalf(s); }
 

@@ -148,9 +148,9 @@ def argmax_rows(logits, out_idx=None, out_val=None, stream=None):
     return out_idx, out_val
 
 
-def i8_quant(x, blk=False, ref_layout=False, stream=None):
-    """Activation quantizer: x f16 [M][K] -> (a8 int8, sa fp32). ref_layout: the reference A8 fragment
-    layout (M = 256, r4d_trellis_i8_quant_act / _row); else plain [M][K] (r4d_i8_quant_act_plain)."""
+def i8_quant(x, blk=False, ref_layout=True, stream=None):
+    """Activation quantizer: x f16 [M][K] -> (a8 int8, sa fp32). ref_layout: the A8 fragment layout (M = 256,
+    r4d_trellis_i8_quant_act / _row, what the GEMMs read); else plain [M][K] (r4d_i8_quant_act_plain)."""
     L = lib()
     M, K = x.shape
     a8 = torch.empty(M * K, dtype=torch.int8, device=x.device)
@@ -164,25 +164,44 @@ def i8_quant(x, blk=False, ref_layout=False, stream=None):
     return a8, sa
 
 
+def i8_pack_w(wp, out=None, stream=None):
+    """Plain int8 [N][K] -> the W8 block layout (r4d_i8_pack_w)."""
+    N, K = wp.shape
+    out = torch.empty(N * K, dtype=torch.int8, device=wp.device) if out is None else out
+    lib().r4d_i8_pack_w(_p(wp), _p(out), N, K, _stream(stream))
+    return out
+
+
 def i8_dense_skg(K, N):
     return lib().r4d_mi355x_i8_skg(K, N)
 
 
-def i8_dense_gemm(a8, sa, w8, sw, K, N, scale_blk=False, skg=None, raw=False, out=None, ws=None, stream=None):
-    """C f16 [256][N] = r4d_gemm_i8_dense, or raw=True the exact int32 sums (r4d_gemm_i8_dense_raw)."""
+class I8Workspace:
+    """ws + the self-resetting tickets of a split int8 launch (one per linear; never two launches in flight)."""
+
+    def __init__(self, N, skg, device):
+        nb = lib().r4d_gemm_i8_dense_ws_bytes(256, N, skg)
+        self.ws = torch.empty(max(1, nb // 4), dtype=torch.int32, device=device)
+        self.tickets = torch.zeros(max(1, N // 128), dtype=torch.int32, device=device)
+
+
+def i8_dense_gemm(a8, sa, w8, sw, K, N, scale_mode=0, skg=None, raw=False, out=None, work=None, stream=None):
+    """C f16 [256][N] = r4d_gemm_i8_dense (a8 A8 layout, w8 W8 block layout), or raw=True the exact int32
+    sums (r4d_gemm_i8_dense_raw)."""
     L = lib()
     M = 256
     skg = i8_dense_skg(K, N) if skg is None else skg
     msg = L.r4d_gemm_i8_dense_check(M, K, N, skg)
     if msg:
         raise ValueError(msg.decode())
-    if ws is None and (skg > 1 or raw):
-        ws = torch.empty(L.r4d_gemm_i8_dense_ws_bytes(M, N, skg) // 4, dtype=torch.int32, device=a8.device)
+    if work is None:
+        work = I8Workspace(N, skg, a8.device)
     if out is None:
         out = torch.empty((M, N), dtype=torch.int32 if raw else torch.float16, device=a8.device)
     st = _stream(stream)
     if raw:
-        L.r4d_gemm_i8_dense_raw(_p(a8), _p(w8), _p(out), _p(ws), M, K, N, skg, st)
+        L.r4d_gemm_i8_dense_raw(_p(a8), _p(w8), _p(out), _p(work.ws), _p(work.tickets), M, K, N, skg, st)
     else:
-        L.r4d_gemm_i8_dense(_p(a8), _p(sa), _p(w8), _p(sw), _p(out), _p(ws), M, K, N, skg, int(scale_blk), st)
+        L.r4d_gemm_i8_dense(_p(a8), _p(sa), _p(w8), _p(sw), _p(out), _p(work.ws), _p(work.tickets), M, K, N, skg,
+                            scale_mode, st)
     return out

@@ -18,6 +18,10 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=o
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I" + CSRC, "-I" + os.path.join(ROOT, "include"), "-Wall", "-Wno-unused-function"]
 
+# Per-source extra flags. int8.hip: the MFMA accumulators stay in VGPRs (the AGPR form of the int8 MFMA
+# does not tie its destination to srcC, and the allocator then rotates 128 accumulators through copies).
+EXTRA = {"int8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
+
 
 def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
@@ -30,7 +34,7 @@ def build(verbose=False, jobs=8):
     for src in sources():
         obj = os.path.join(objdir, os.path.basename(src) + ".o")
         objs.append(obj)
-        cmd = [HIPCC] + FLAGS + ["-c", src, "-o", obj]
+        cmd = [HIPCC] + FLAGS + EXTRA.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))

@@ -42,8 +42,9 @@ SIGS = {
     "r4d_trellis_i8_quant_act": (None, [I64, I64, I64, I32, I64, I32, I64]),
     "r4d_trellis_i8_quant_act_row": (None, [I64, I64, I64, I32, I64, I32, I64]),
     "r4d_i8_quant_act_plain": (None, [I64, I64, I64, I32, I32, I32, I64]),
-    "r4d_gemm_i8_dense": (None, [I64] * 6 + [I32] * 5 + [I64]),
-    "r4d_gemm_i8_dense_raw": (None, [I64] * 4 + [I32] * 4 + [I64]),
+    "r4d_gemm_i8_dense": (None, [I64] * 7 + [I32] * 5 + [I64]),
+    "r4d_gemm_i8_dense_raw": (None, [I64] * 5 + [I32] * 4 + [I64]),
+    "r4d_i8_pack_w": (None, [I64, I64, I32, I32, I64]),
     "r4d_gemm_i8_dense_check": (CSTR, [I32] * 4),
     "r4d_gemm_i8_dense_ws_bytes": (SZ, [I32] * 3),
     "r4d_mi355x_i8_skg": (I32, [I32, I32]),

@@ -53,6 +53,8 @@ _SIGS = {
     "r4o_i8_gemm_ref": (None, [P, P, P, P, I32, I32, I32, I32, P, I32]),
     "r4o_a8_offset": (C.c_size_t, [I32, I32, I32]),
     "r4o_pack_a8": (None, [P, I32, P]),
+    "r4o_w8_offset": (C.c_size_t, [I32, I32, I32]),
+    "r4o_pack_w8": (None, [P, I32, I32, P]),
     "r4o_w4_quantize": (None, [P, I32, I32, I32, P, P, P]),
     "r4o_w4_pack": (None, [P, I32, I32, P]),
     "r4o_w4_pack_scales": (None, [P, P, I32, I32, I32, P]),
@@ -79,6 +81,7 @@ _REF_SIGS = {
     "ref_i8_quant_act_row": (None, [P, I32, P, P]),
     "ref_i8_gemm": (None, [P, P, P, P, I32, I32, I32, I32, P]),
     "ref_a8_offset": (C.c_size_t, [I32, I32, I32]),
+    "ref_w8_offset": (C.c_size_t, [I32, I32, I32]),
     "ref_i8_quant_w": (C.c_int8, [C.c_uint16, C.c_uint16]),
     "ref_i8_rs_half": (C.c_uint16, [C.c_float]),
     "ref_w4_quantize_pack": (None, [P, I32, I32, I32, P, P]),

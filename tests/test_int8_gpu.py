@@ -49,51 +49,96 @@ def test_quantizers_bit_exact(blk, ref_layout):
         assert np.array_equal(got.reshape(256, K), ap)
 
 
-@pytest.mark.parametrize("K,N,skg", [(512, 256, 1), (1024, 384, 2), (2048, 128, 4), (640, 512, 5)])
+def _a8(ap):
+    out = np.empty(ap.size, np.int8)
+    O.lib().r4o_pack_a8(ptr(ap), ap.shape[1], ptr(out))
+    return out
+
+
+def test_pack_w_matches_oracle():
+    banner("i8 pack_w")
+    rng = np.random.default_rng(3)
+    N, K = 96, 384
+    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    got = api.i8_pack_w(dev(w)).cpu().numpy()
+    ref = np.empty(N * K, np.int8)
+    O.lib().r4o_pack_w8(ptr(w), N, K, ptr(ref))
+    assert np.array_equal(got, ref)
+
+
+def _i32_ref(a, w):
+    ref = np.empty((256, w.shape[0]), np.int32)
+    O.lib().r4o_i8_gemm_i32(ptr(a), ptr(w), 256, w.shape[0], a.shape[1], ptr(ref), 0)
+    return ref
+
+
+@pytest.mark.parametrize("K,N,skg", [(128, 128, 1), (512, 256, 1), (1024, 384, 2), (2048, 128, 4), (640, 512, 5),
+                                     (384, 256, 3)])
 def test_dense_int32_exact(K, N, skg):
     banner("i8 raw", K, N, skg)
     rng = np.random.default_rng(K + N)
     a = rng.integers(-127, 128, (256, K)).astype(np.int8)
     w = rng.integers(-127, 128, (N, K)).astype(np.int8)
-    c = api.i8_dense_gemm(dev(a), None, dev(w), None, K, N, skg=skg, raw=True)
-    torch.cuda.synchronize()
-    ref = np.empty((256, N), np.int32)
-    O.lib().r4o_i8_gemm_i32(ptr(a), ptr(w), 256, N, K, ptr(ref), 0)
-    assert np.array_equal(c.cpu().numpy(), ref)
+    w8 = api.i8_pack_w(dev(w))
+    work = api.I8Workspace(N, skg, w8.device)
+    for _ in range(2):       # the tickets reset themselves: a second launch on the same workspace
+        c = api.i8_dense_gemm(dev(_a8(a)), None, w8, None, K, N, skg=skg, raw=True, work=work)
+        torch.cuda.synchronize()
+        assert np.array_equal(c.cpu().numpy(), _i32_ref(a, w))
+    assert int(work.tickets.abs().sum()) == 0
 
 
-@pytest.mark.parametrize("blk", [False, True])
-@pytest.mark.parametrize("K,N,skg", [(1024, 256, 1), (2048, 384, 2)])
-def test_dense_scaled(blk, K, N, skg):
-    banner("i8 dense", blk, K, N, skg)
-    x, w8, sw = WL.int8_case(K, N, 7)
-    a8, sa = api.i8_quant(dev(x.view(np.uint16)), blk)
-    c = api.i8_dense_gemm(a8, sa, dev(w8), dev(sw), K, N, scale_blk=blk, skg=skg)
+def test_dense_int32_extremes():
+    """Saturated operands: |sum| up to K 127^2 (K = 17408: 2.8e8 < 2^31), every sign combination."""
+    K, N = 17408, 128
+    a = np.full((256, K), 127, np.int8)
+    a[1::2] = -127
+    w = np.full((N, K), 127, np.int8)
+    w[::3] = -127
+    w[5, ::2] = 0
+    c = api.i8_dense_gemm(dev(_a8(a)), None, api.i8_pack_w(dev(w)), None, K, N, skg=4, raw=True)
     torch.cuda.synchronize()
+    assert np.array_equal(c.cpu().numpy(), _i32_ref(a, w))
+
+
+def _oracle_mode(x, w8, sw, mode):
+    """The oracle's f64 result for scale mode 0 (row x column), 1 (per-128 activation x column) or 2 (per-128
+    both: sw is [K/128][N])."""
+    blk = mode != 0
     sa_ref, ap = _oracle_quant(x, blk)
-    ref = np.empty((256, N), np.float64)
-    O.lib().r4o_i8_gemm_ref(ptr(ap), ptr(sa_ref), ptr(w8), ptr(sw), 256, N, K, 2 if blk else 3, ptr(ref), 0)
-    assert close_rel(c.float().cpu().numpy(), ref, 1e-3, 1e-4) <= 1.0
+    ref = np.empty((256, w8.shape[0]), np.float64)
+    mask = {0: 3, 1: 2, 2: 0}[mode]
+    O.lib().r4o_i8_gemm_ref(ptr(ap), ptr(sa_ref), ptr(w8), ptr(sw), 256, w8.shape[0], x.shape[1], mask, ptr(ref), 0)
+    return ref
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("K,N,skg", [(1024, 256, 1), (2048, 384, 2), (1536, 128, 3)])
+def test_dense_scaled(mode, K, N, skg):
+    banner("i8 dense", mode, K, N, skg)
+    x, w8, sw = WL.int8_case(K, N, 7)
+    if mode == 2:
+        sw = np.random.default_rng(8).lognormal(np.log(0.01), 0.3, (K // 128, N)).astype(np.float32)
+    a8, sa = api.i8_quant(dev(x.view(np.uint16)), mode != 0)
+    c = api.i8_dense_gemm(a8, sa, api.i8_pack_w(dev(w8)), dev(sw.reshape(-1)), K, N, scale_mode=mode, skg=skg)
+    torch.cuda.synchronize()
+    assert close_rel(c.float().cpu().numpy(), _oracle_mode(x, w8, sw, mode), 1e-3, 1e-4) <= 1.0
 
 
 @pytest.mark.parametrize("K,N", [(5120, 17408), (17408, 5120)])
 def test_config4(K, N):
-    """Both config-4 shapes: int32 accumulators exact, f16 outputs within tolerance for both scale
-    variants."""
+    """Both config-4 shapes at the planner's split: the quantized bytes exact, the int32 accumulators exact,
+    the f16 outputs within tolerance for the row and the per-128 activation scales."""
     x, w8, sw = WL.int8_case(K, N, 11)
-    w_d = dev(w8)
-    for blk in (False, True):
-        banner("config4", K, N, blk)
-        a8, sa = api.i8_quant(dev(x.view(np.uint16)), blk)
-        c = api.i8_dense_gemm(a8, sa, w_d, dev(sw), K, N, scale_blk=blk)
-        raw = api.i8_dense_gemm(a8, None, w_d, None, K, N, raw=True) if not blk else None
+    w_d = api.i8_pack_w(dev(w8))
+    x_d = dev(x.view(np.uint16))
+    raw = api.i8_dense_gemm(api.i8_quant(x_d, False)[0], None, w_d, None, K, N, raw=True)
+    torch.cuda.synchronize()
+    _, ap = _oracle_quant(x, False)
+    assert np.array_equal(raw.cpu().numpy(), _i32_ref(ap, w8))
+    for mode in (0, 1):
+        banner("config4", K, N, mode)
+        a8, sa = api.i8_quant(x_d, mode != 0)
+        c = api.i8_dense_gemm(a8, sa, w_d, dev(sw), K, N, scale_mode=mode)
         torch.cuda.synchronize()
-        sa_ref, ap = _oracle_quant(x, blk)
-        assert np.array_equal(a8.cpu().numpy().reshape(256, K), ap)
-        if raw is not None:
-            ref_i = np.empty((256, N), np.int32)
-            O.lib().r4o_i8_gemm_i32(ptr(ap), ptr(w8), 256, N, K, ptr(ref_i), 0)
-            assert np.array_equal(raw.cpu().numpy(), ref_i)
-        ref = np.empty((256, N), np.float64)
-        O.lib().r4o_i8_gemm_ref(ptr(ap), ptr(sa_ref), ptr(w8), ptr(sw), 256, N, K, 2 if blk else 3, ptr(ref), 0)
-        assert close_rel(c.float().cpu().numpy(), ref, 1e-3, 1e-4) <= 1.0
+        assert close_rel(c.float().cpu().numpy(), _oracle_mode(x, w8, sw, mode), 1e-3, 1e-4) <= 1.0

@@ -217,6 +217,17 @@ def test_a8_layout_is_permutation(olib):
     assert np.array_equal(np.sort(offs), np.arange(256 * K))
 
 
+def test_w8_layout_is_permutation(olib):
+    K, N = 256, 128
+    offs = np.array([olib.r4o_w8_offset(n, k, K) for n in range(N) for k in range(K)])
+    assert np.array_equal(np.sort(offs), np.arange(N * K))
+    # a lane's 16 bytes of fragment F are one column; its 8 bytes per half are 4 + 4 consecutive k
+    assert olib.r4o_w8_offset(0, 0, K) == 0 and olib.r4o_w8_offset(0, 3, K) == 3
+    assert olib.r4o_w8_offset(0, 8, K) == 4 and olib.r4o_w8_offset(0, 4, K) == 16 * 16
+    assert olib.r4o_w8_offset(8, 0, K) == 8 and olib.r4o_w8_offset(16, 0, K) == 16 * 8
+    assert olib.r4o_w8_offset(32, 0, K) == (K // 16) * 512 and olib.r4o_w8_offset(0, 16, K) == 512
+
+
 # ---- w4a16: the reference's committed byte fixtures (tests/convert/test_pack_bytes.cpp:78-99) --------
 def test_w4a16_pack_matches_reference_fixtures(olib):
     from safetensors.torch import load_file

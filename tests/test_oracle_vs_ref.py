@@ -90,6 +90,9 @@ def test_int8_quantizers_and_gemm(olib, rlib):
         assert np.array_equal(s1, s2) and np.array_equal(a1, a2)
     for r, k in [(0, 0), (17, 5), (200, 255), (63, 130)]:
         assert olib.r4o_a8_offset(r, k, K) == rlib.ref_a8_offset(r, k, K)
+    for n in range(0, N, 7):
+        for k in range(0, K, 5):
+            assert olib.r4o_w8_offset(n, k, K) == rlib.ref_w8_offset(n, k, K)
     A = rng.integers(-127, 128, (16, K)).astype(np.int8)
     W = rng.integers(-127, 128, (N, K)).astype(np.int8)
     sa = rng.random(K // 128 * 16).astype(np.float32)
