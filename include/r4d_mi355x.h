@@ -110,8 +110,8 @@ void r4d_trellis_i8_quant_act(int64_t x, int64_t a8, int64_t sa, int parts, int6
 /* r4d.h:517-518 r4d_trellis_i8_quant_act_row: the same with one scale per row, SA [256] per part. */
 void r4d_trellis_i8_quant_act_row(int64_t x, int64_t a8, int64_t sa, int parts, int64_t part_stride, int K,
                                   int64_t stream);
-/* No reference counterpart (the dense GEMM's operand): a8 plain [M][K]; blk != 0: sa [K/128][M], else
- * sa [M]. */
+/* No reference counterpart: the same quantizers for any M into a plain row-major a8 [M][K] (for callers
+ * that keep int8 activations row-major); blk != 0: sa [K/128][M], else sa [M]. */
 void r4d_i8_quant_act_plain(int64_t x, int64_t a8, int64_t sa, int M, int K, int blk, int64_t stream);
 /* No reference counterpart as an entry: the reference has the dense form only as its bench kernel
  * (i8g_kernel<TRELLIS = false>, r4d_trellis_i8.h:19-21), with the same operand layouts. C f16 [256][N].
