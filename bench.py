@@ -37,6 +37,9 @@ def parse():
     ap.add_argument("--no-m256", action="store_true", help="skip the M = 256 prefill GEMM leg")
     ap.add_argument("--no-w4", action="store_true", help="skip the w4a16 LM-head leg")
     ap.add_argument("--no-i8", action="store_true", help="skip the int8 prefill GEMM leg")
+    ap.add_argument("--pmc", action="store_true",
+                    help="counter pass for rocprofv3 --pmc: a 512 MiB copy (calibration) and two eager "
+                         "passes of the GEMV launches; prints no JSON line")
     return ap.parse_args()
 
 
@@ -91,6 +94,21 @@ def main():
     for c in range(copies):   # eager once: A is valid, tickets settle
         step(c)
     torch.cuda.synchronize()
+    if args.pmc:
+        # calibration: a plain device copy of a known size (the counters' bytes per algorithmic byte)
+        src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        for _ in range(2):
+            for c in range(copies):
+                for L in lin:
+                    gemv(L, c)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_pass": "done", "copy_bytes": 512 << 20,
+                          "shapes": {L["name"]: [L["K"], L["N"]] for L in lin}}), flush=True)
+        return
 
     def capture(fn):
         g = torch.cuda.CUDAGraph()
@@ -166,7 +184,7 @@ def main():
                    "M": M, "KB": KB, "weight_bytes_per_step": layer_wbytes,
                    "step": "input transform + trellis GEMV (FWHT/svh epilogue, bf16 out) per projection"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic("tq_gemv_kernel", KB, M),
                      "kernel": "tq_gemv_kernel", "avg_launch_us": round(gemv_ms * 1e3 / len(lin), 3),
                      "per_shape_GBs": per_shape},
         "cpu_baseline": cpu,
@@ -287,6 +305,21 @@ def bench_w4a16(api, WL, R=4):
         torch.cuda.empty_cache()
     return {"metric": "w4a16 LM head (N=248320, K=5120) effective HBM GB/s", "kernel": "w4_kernel",
             "peak_GBs": HBM_PEAK_GBS, "cases": res}
+
+
+def _traffic(kernel, KB, M):
+    """HBM bytes per launch of `kernel` (mean over the config-1 shapes), from the committed summary of the
+    two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE), each scaled by the same counter's reading for a
+    copy of known size; None when no summary matches this configuration."""
+    path = os.path.join(ROOT, "profiles", "gemv_traffic_config1.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("kernel") != kernel or t.get("KB") != KB or t.get("M") != M:
+        return None
+    return t.get("hbm_bytes_per_launch")
 
 
 def _graph_ms(fn, R, per):
