@@ -26,199 +26,236 @@ __device__ __forceinline__ r4_rsrc mk_rsrc(const void* p, unsigned bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
 }
 
-// RT = row tiles per wave (4 at M = 256, 2 at M = 128).
+// A workgroup is 8 waves over all M rows x one 128-column group x one K slice, in 64-k steps through a
+// double-buffered LDS stage:
+//   * 4 producer waves: producer p loads rows [p M/4, (p+1) M/4) of the step's A (coalesced: 8 lanes per
+//     128-byte row segment) and the words of tile pair p, decodes them, and writes both into the stage;
+//   * 4 math waves: math wave (rh, ch) owns rows [rh M/2, +M/2) x columns [64 ch, +64) of the group =
+//     RT = M / 32 row tiles x 4 column tiles of v_mfma_f32_16x16x32_f16, reading A and B from LDS.
+// A and B are both stored in natural k order (A [row][64 k], B [16-byte chunk of 8 k][column], f16):
+// the decode's fragments (element e of half h <-> k = 8 (e >> 2) + 4 h + (e & 3)) are re-paired
+// in registers into the natural 16-byte chunks k 0-7 and 8-15 of a k-tile before the store. The 16-byte
+// chunk c of row r sits at slot c ^ ((r >> 1) & 7), so the 16 rows a fragment read touches use 16 distinct
+// bank groups.
+constexpr int kM2Waves = 8;
+__device__ __forceinline__ int m2_slot(int r, int c) { return (r * 8 + (c ^ ((r >> 1) & 7))) * 16; }
+// B is [chunk][column] instead: a decode lane writes columns 32 p + 16 t + 8 cs + c, so column bit 3 is
+// flipped on odd 16-column tiles to keep the t = 0 and t = 1 lanes of one write on different banks; a
+// fragment read (16 consecutive columns of one chunk) stays a permutation of 16 bank slots.
+__device__ __forceinline__ int m2_bslot(int n, int c) { return c * 2048 + ((n ^ (((n >> 4) & 1) << 3)) * 16); }
+
 template <int KB, int RT>
-__global__ __launch_bounds__(256, 2) void tq_m256_kernel(
+__global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
     const unsigned short* __restrict__ A0, const unsigned short* __restrict__ A1, int n_split,
     const unsigned* __restrict__ W, const float* __restrict__ svh, void* __restrict__ Cv,
-    float* __restrict__ ws, unsigned* __restrict__ tickets, int M, int K, int N, int SKG, int full,
-    float out_scale) {
+    float* __restrict__ ws, int M, int K, int N, int SKG, int full, float out_scale) {
   constexpr int BLK = 16 * KB;                    // words per (pair, k-tile) block
-  constexpr unsigned kStepBytes = 4 * BLK * 4;
-  __shared__ r4u4 bfrag[2][4][4][64];             // [buf][pair][cs * 2 + h][lane]: 16 KiB x 2
+  constexpr unsigned kStepBytes = 4 * BLK * 4;    // one pair's words per step
+  constexpr int MR = 32 * RT;                     // rows of the launch (128 or 256)
+  constexpr int kA = MR * 128, kStage = kA + 128 * 128;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int group = blockIdx.x, ky = blockIdx.y;
   const int KT = K >> 4, ktw = KT / SKG, kt0 = ky * ktw;
   const int nst = ktw >> 2;
-  const int q = lane >> 4, t = (lane >> 3) & 1, c = lane & 7, mrow = lane & 15;
-  const unsigned short* __restrict__ A = group * 128 >= n_split ? A1 : A0;
-
-  // this wave's weights: pair group * 4 + wave, k-tiles [kt0, kt0 + ktw)
-  const int pair = group * 4 + wave;
-  const r4_rsrc wr = mk_rsrc(W + ((size_t)pair * KT + kt0) * BLK, (unsigned)ktw * BLK * 4u);
-  const unsigned tile = (unsigned)(q * 16 * KB + t * 8 * KB);
-  const unsigned own = (tile + KB * c) * 4u, hist = (tile + (KB * c - 1 + 8 * KB) % (8 * KB)) * 4u;
-  // this wave's A rows: 16 RT rows from wave * 16 RT; lane row mrow of each tile, k-tile q of a step
-  const r4_rsrc ar = mk_rsrc(A, (unsigned)((size_t)M * K * 2));
-  unsigned aoff[RT];
-#pragma unroll
-  for (int i = 0; i < RT; ++i)
-    aoff[i] = (unsigned)(((size_t)(wave * 16 * RT + i * 16 + mrow) * K + (size_t)(kt0 + q) * 16) * 2);
-
-  auto load_w = [&](unsigned (&w)[KB + 1], int st) {
-    const unsigned so = (unsigned)st * kStepBytes;
-    if constexpr (KB == 4) {
-      const r4u4 v = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(wr, own + so, 0, 0));
-      w[1] = v[0]; w[2] = v[1]; w[3] = v[2]; w[4] = v[3];
-    } else {
-#pragma unroll
-      for (int i = 0; i < KB; ++i) w[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(wr, own + so + 4 * i, 0, 0);
-    }
-    w[0] = __builtin_amdgcn_raw_buffer_load_b32(wr, hist + so, 0, 0);
-  };
-  auto load_a = [&](r4u4 (&a)[RT][2], int st) {
-    const unsigned so = (unsigned)st * 4 * 32;   // 4 k-tiles of 16 halves
-#pragma unroll
-    for (int i = 0; i < RT; ++i) {
-      a[i][0] = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(ar, aoff[i] + so, 0, 0));
-      a[i][1] = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(ar, aoff[i] + so + 16, 0, 0));
-    }
-  };
-
-  r4f4 acc[RT][4][2];
-#pragma unroll
-  for (int i = 0; i < RT; ++i)
-#pragma unroll
-    for (int p = 0; p < 4; ++p) acc[i][p][0] = acc[i][p][1] = (r4f4){0.f, 0.f, 0.f, 0.f};
-
-  unsigned wcur[KB + 1], wnext[KB + 1];
-  r4u4 acur[RT][2], anext[RT][2];
-  if (nst > 0) {
-    load_w(wcur, 0);
-    load_a(acur, 0);
-  }
-  for (int st = 0; st < nst; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < nst) {
-      load_w(wnext, st + 1);
-      load_a(anext, st + 1);
-    }
-    {
-      unsigned d[2][2][4];
-      r4_decode<KB>(wcur, d);
-#pragma unroll
-      for (int cs = 0; cs < 2; ++cs)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          bfrag[buf][wave][cs * 2 + h][lane] = (r4u4){d[cs][h][0], d[cs][h][1], d[cs][h][2], d[cs][h][3]};
-    }
-    __syncthreads();
-    // A fragments of this step: h = 0 takes k 0..3 and 8..11 of the lane's k-tile, h = 1 the rest
-    r4h8 af[RT][2];
-#pragma unroll
-    for (int i = 0; i < RT; ++i) {
-      const r4u4 lo = acur[i][0], hi = acur[i][1];
-      af[i][0] = __builtin_bit_cast(r4h8, (r4u4){lo[0], lo[1], hi[0], hi[1]});
-      af[i][1] = __builtin_bit_cast(r4h8, (r4u4){lo[2], lo[3], hi[2], hi[3]});
-    }
-#pragma unroll
-    for (int p = 0; p < 4; ++p)
-#pragma unroll
-      for (int cs = 0; cs < 2; ++cs)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const r4h8 b = __builtin_bit_cast(r4h8, bfrag[buf][p][cs * 2 + h][lane]);
-#pragma unroll
-          for (int i = 0; i < RT; ++i) acc[i][p][cs] = r4_mfma16(af[i][h], b, acc[i][p][cs]);
-        }
-    if (st + 1 < nst) {
-#pragma unroll
-      for (int i = 0; i <= KB; ++i) wcur[i] = wnext[i];
-#pragma unroll
-      for (int i = 0; i < RT; ++i) { acur[i][0] = anext[i][0]; acur[i][1] = anext[i][1]; }
-    }
-  }
-
-  // Lane l holds, for row tile i, rows 16 i + 4 (l >> 4) + j (+ this wave's base) and, for pair p
-  // and slot cs, group column 32 p + 16 (nb >> 3) + (nb & 7) + 8 cs with nb = l & 15.
-  const int nb = lane & 15, rq = lane >> 4;
   const int n0 = group * 128;
-  const int row0 = wave * 16 * RT;
-  if (SKG > 1) {
-    // split K: this slice's sums to ws[ky]; tq_m256_finish adds the slices after this launch
-    float* wsy = ws + (size_t)ky * M * N;
+  const unsigned short* __restrict__ A = n0 >= n_split ? A1 : A0;
+
+  if (wave >= 4) {
+    // ---- producer p
+    const int p = wave - 4;
+    const int q = lane >> 4, t = (lane >> 3) & 1, c = lane & 7;
+    const int pair = group * 4 + p;
+    const r4_rsrc wr = mk_rsrc(W + ((size_t)pair * KT + kt0) * BLK, (unsigned)ktw * BLK * 4u);
+    const unsigned tile = (unsigned)(q * 16 * KB + t * 8 * KB);
+    const unsigned own = (tile + KB * c) * 4u, hist = (tile + (KB * c - 1 + 8 * KB) % (8 * KB)) * 4u;
+    constexpr int RA = MR / 4, AU = RA / 8;       // rows per producer; 16-byte loads per lane per step
+    const r4_rsrc ar = mk_rsrc(A, (unsigned)((size_t)MR * K * 2));
+    const int ar0 = p * RA + (lane >> 3), ac = lane & 7;
+    const unsigned aoff = (unsigned)(((size_t)ar0 * K + (size_t)kt0 * 16 + ac * 8) * 2);
+
+    struct St {
+      unsigned w[KB + 1];
+      r4u4 a[AU];
+    };
+    auto load = [&](St& s, int st) {
+      const int sc = min(st, nst - 1);
+      const unsigned so = (unsigned)sc * kStepBytes;
+      if constexpr (KB == 4) {
+        const r4u4 v = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(wr, own + so, 0, 0));
+        s.w[1] = v[0]; s.w[2] = v[1]; s.w[3] = v[2]; s.w[4] = v[3];
+      } else {
 #pragma unroll
-    for (int i = 0; i < RT; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = row0 + 16 * i + 4 * rq + j;
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-#pragma unroll
-          for (int cs = 0; cs < 2; ++cs)
-            wsy[(size_t)r * N + n0 + 32 * p + 16 * (nb >> 3) + (nb & 7) + 8 * cs] = acc[i][p][cs][j];
+        for (int i = 0; i < KB; ++i) s.w[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(wr, own + so + 4 * i, 0, 0);
       }
+      s.w[0] = __builtin_amdgcn_raw_buffer_load_b32(wr, hist + so, 0, 0);
+#pragma unroll
+      for (int u = 0; u < AU; ++u)
+        s.a[u] = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              ar, aoff + (unsigned)(u * 8 * K * 2) + (unsigned)sc * 128u, 0, 0));
+    };
+    auto put = [&](const St& s, int st) {
+      unsigned char* stg = lds + (st & 1) * kStage;
+#pragma unroll
+      for (int u = 0; u < AU; ++u) *(r4u4*)(stg + m2_slot(ar0 + 8 * u, ac)) = s.a[u];
+      unsigned d[2][2][4];
+      r4_decode<KB>(s.w, d);
+#pragma unroll
+      for (int cs = 0; cs < 2; ++cs) {
+        const int n = 32 * p + 16 * t + 8 * cs + c;
+        *(r4u4*)(stg + kA + m2_bslot(n, 2 * q)) = (r4u4){d[cs][0][0], d[cs][0][1], d[cs][1][0], d[cs][1][1]};
+        *(r4u4*)(stg + kA + m2_bslot(n, 2 * q + 1)) = (r4u4){d[cs][0][2], d[cs][0][3], d[cs][1][2], d[cs][1][3]};
+      }
+    };
+    constexpr int PF = 2;
+    St ring[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) load(ring[i], i);
+    // stage 0 <- step 0; then, after barrier st, stage (st + 1) & 1 <- step st + 1. In the steady loop a
+    // put past the last step writes the (clamped) last step into the stage nobody reads any more, so the
+    // loop carries no branch; the remainder of nst % PF steps runs in the tail.
+    put(ring[0], 0);
+    load(ring[0], PF);
+    int st = 0;
+    for (; st + PF <= nst; st += PF) {
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        put(ring[(i + 1) % PF], st + i + 1);
+        load(ring[(i + 1) % PF], st + i + 1 + PF);
+      }
+    }
+    for (; st < nst; ++st) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      if (st + 1 < nst) put(ring[(st + 1) % PF == 0 ? 0 : 1], st + 1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (SKG == 1 && full) {      // the epilogue's two exchange rounds
+#pragma unroll 1
+      for (int r = 0; r < 2 * 2; ++r) __syncthreads();
+    }
     return;
   }
-  float* Cf = (float*)Cv;
-  unsigned short* Cb = (unsigned short*)Cv;
-  if (!full) {
-#pragma unroll
-    for (int i = 0; i < RT; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = row0 + 16 * i + 4 * rq + j;
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-#pragma unroll
-          for (int cs = 0; cs < 2; ++cs)
-            Cf[(size_t)r * N + n0 + 32 * p + 16 * (nb >> 3) + (nb & 7) + 8 * cs] = acc[i][p][cs][j];
-      }
-    return;
-  }
-  // FWHT-128 over each row's group columns, stage lg = 0..6 on column bit lg: bits 0-2 are lane bits
-  // 0-2 (partner lane ^ 1, 2, 4), bit 3 is cs, bit 4 is lane bit 3 (partner lane ^ 8), bits 5-6 are p.
-  // The lower index keeps a + b, the upper takes a - b.
+
+  // ---- math wave (rh, ch)
+  const int rh = wave >> 1, ch = wave & 1;
+  const int r16 = lane & 15, g = lane >> 4;
+  r4f4 acc[RT][4];
 #pragma unroll
   for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) acc[i][ct] = (r4f4){0.f, 0.f, 0.f, 0.f};
+  const int arow = rh * (MR / 2) + r16, bcol = 64 * ch + r16;
+  // Software pipeline by half steps (kh = 0, 1 = the step's two 32-k halves): the fragments of the next
+  // half are read while the current half's MFMAs run, and the barrier sits between the halves, so neither
+  // the LDS latency nor the barrier wait idles the MFMA pipe. The last step is peeled (no barrier after it:
+  // the producers meet nst barriers too).
+  auto read_half = [&](r4h8 (&af)[RT], r4h8 (&bf)[4], int st, int kh) {
+    const unsigned char* stg = lds + (st & 1) * kStage;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) bf[ct] = *(const r4h8*)(stg + kA + m2_bslot(bcol + 16 * ct, 4 * kh + g));
+#pragma unroll
+    for (int i = 0; i < RT; ++i) af[i] = *(const r4h8*)(stg + m2_slot(arow + 16 * i, 4 * kh + g));
+  };
+  auto mfma_half = [&](const r4h8 (&af)[RT], const r4h8 (&bf)[4]) {
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) acc[i][ct] = r4_mfma16(af[i], bf[ct], acc[i][ct]);
+  };
+  r4h8 af0[RT], bf0[4], af1[RT], bf1[4];
+  __builtin_amdgcn_s_barrier();          // B_0: stage 0 landed
+  read_half(af0, bf0, 0, 0);
+  for (int st = 0; st + 1 < nst; ++st) {
+    read_half(af1, bf1, st, 1);
+    mfma_half(af0, bf0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's reads of stage st done
+    __builtin_amdgcn_s_barrier();                        // B_(st+1): stage st + 1 landed
+    read_half(af0, bf0, st + 1, 0);
+    mfma_half(af1, bf1);
+  }
+  if (nst > 0) {
+    read_half(af1, bf1, nst - 1, 1);
+    mfma_half(af0, bf0);
+    mfma_half(af1, bf1);
+  }
+
+  // lane holds, for row tile i and column tile ct, rows rh M/2 + 16 i + 4 g + j, column 64 ch + 16 ct + r16
+  const int row0 = rh * (MR / 2);
+  if (SKG > 1 || !full) {
+    float* dst = SKG > 1 ? ws + (size_t)ky * M * N : (float*)Cv;
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = row0 + 16 * i + 4 * g + j;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) dst[(size_t)r * N + n0 + 64 * ch + 16 * ct + r16] = acc[i][ct][j];
+      }
+    return;
+  }
+  // FWHT-128 over the group's columns, stages lg = 0..6 in order on column bit lg (the lower index keeps
+  // a + b, the upper takes a - b): bits 0-3 are lane bits 0-3, bits 4-5 the column tile, bit 6 the
+  // column half ch, exchanged with the partner wave (rh, ch ^ 1) through LDS in two rounds of RT / 2 row
+  // tiles (every wave of the workgroup meets both barriers of a round).
+#pragma unroll
+  for (int i = 0; i < RT; ++i) {
+    auto lane_stage = [&](int mask) {
+      const bool upper = (lane & mask) != 0;
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float o = __shfl_xor(acc[i][ct][j], mask, 64);
+          acc[i][ct][j] = upper ? o - acc[i][ct][j] : acc[i][ct][j] + o;
+        }
+    };
+    lane_stage(1);
+    lane_stage(2);
+    lane_stage(4);
+    lane_stage(8);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float v[4][2];
-#pragma unroll
-      for (int p = 0; p < 4; ++p) { v[p][0] = acc[i][p][0][j]; v[p][1] = acc[i][p][1][j]; }
-      auto lane_stage = [&](int mask) {
-        const bool upper = (lane & mask) != 0;
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-#pragma unroll
-          for (int cs = 0; cs < 2; ++cs) {
-            const float o = __shfl_xor(v[p][cs], mask, 64);
-            v[p][cs] = upper ? o - v[p][cs] : v[p][cs] + o;
-          }
-      };
-      lane_stage(1);
-      lane_stage(2);
-      lane_stage(4);
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {            // bit 3: cs
-        const float a = v[p][0], b = v[p][1];
-        v[p][0] = a + b;
-        v[p][1] = a - b;
-      }
-      lane_stage(8);
-#pragma unroll
-      for (int cs = 0; cs < 2; ++cs) {         // bit 5: p ^ 1
-        const float a0 = v[0][cs], b0 = v[1][cs], a1 = v[2][cs], b1 = v[3][cs];
-        v[0][cs] = a0 + b0; v[1][cs] = a0 - b0;
-        v[2][cs] = a1 + b1; v[3][cs] = a1 - b1;
-      }
-#pragma unroll
-      for (int cs = 0; cs < 2; ++cs) {         // bit 6: p ^ 2
-        const float a0 = v[0][cs], b0 = v[2][cs], a1 = v[1][cs], b1 = v[3][cs];
-        v[0][cs] = a0 + b0; v[2][cs] = a0 - b0;
-        v[1][cs] = a1 + b1; v[3][cs] = a1 - b1;
-      }
-      const int r = row0 + 16 * i + 4 * rq + j;
-#pragma unroll
-      for (int p = 0; p < 4; ++p)
-#pragma unroll
-        for (int cs = 0; cs < 2; ++cs) {
-          const int n = n0 + 32 * p + 16 * (nb >> 3) + (nb & 7) + 8 * cs;
-          const float y = v[p][cs] * svh[n];
-          Cb[(size_t)r * N + n] = r4_bf16_rn(y * out_scale);
-        }
+      float a0 = acc[i][0][j], b0 = acc[i][1][j], a1 = acc[i][2][j], b1 = acc[i][3][j];   // bit 4: ct ^ 1
+      acc[i][0][j] = a0 + b0; acc[i][1][j] = a0 - b0; acc[i][2][j] = a1 + b1; acc[i][3][j] = a1 - b1;
+      a0 = acc[i][0][j]; b0 = acc[i][2][j]; a1 = acc[i][1][j]; b1 = acc[i][3][j];           // bit 5: ct ^ 2
+      acc[i][0][j] = a0 + b0; acc[i][2][j] = a0 - b0; acc[i][1][j] = a1 + b1; acc[i][3][j] = a1 - b1;
     }
+  }
+  float sv[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) sv[ct] = svh[n0 + 64 * ch + 16 * ct + r16];
+  unsigned short* Cb = (unsigned short*)Cv;
+  constexpr int RR = RT / 2;                     // row tiles per exchange round
+  r4f4* xch = (r4f4*)lds;                        // [wave 0..3][RR][ct][lane]
+#pragma unroll
+  for (int rd = 0; rd < 2; ++rd) {
+    __syncthreads();                             // the stages (or the previous round) are no longer read
+#pragma unroll
+    for (int ii = 0; ii < RR; ++ii)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) xch[((wave * RR + ii) * 4 + ct) * 64 + lane] = acc[rd * RR + ii][ct];
+    __syncthreads();
+    const int partner = wave ^ 1;
+#pragma unroll
+    for (int ii = 0; ii < RR; ++ii) {
+      const int i = rd * RR + ii;
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const r4f4 o = xch[((partner * RR + ii) * 4 + ct) * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float v = ch ? o[j] - acc[i][ct][j] : acc[i][ct][j] + o[j];
+          const int r = row0 + 16 * i + 4 * g + j;
+          const int n = n0 + 64 * ch + 16 * ct + r16;
+          Cb[(size_t)r * N + n] = r4_bf16_rn((v * sv[ct]) * out_scale);
+        }
+      }
+    }
+  }
 }
 
 // The split form's second pass: a workgroup per (128-column group, 32 rows) sums the SKG slices of
@@ -274,17 +311,27 @@ std::string m256_check(int M, int K, int N, int n_split, int KB, int SKG) {
   return "";
 }
 
+template <int KB, int RT>
+void m256_launch_rt(const unsigned short* a0, const unsigned short* a1, int n_split, const unsigned* w,
+                    const float* svh, void* c, float* ws, int M, int K, int N, int SKG, int full, float out_scale,
+                    hipStream_t st) {
+  constexpr unsigned lds = 2 * (32 * RT * 128 + 128 * 128);
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute((const void*)tq_m256_kernel<KB, RT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds);
+    attr = true;
+  }
+  hipLaunchKernelGGL((tq_m256_kernel<KB, RT>), dim3(N / 128, SKG), dim3(64 * kM2Waves), lds, st, a0, a1, n_split, w,
+                     svh, c, ws, M, K, N, SKG, full, out_scale);
+}
 template <int KB>
 void m256_launch(int M, const unsigned short* a0, const unsigned short* a1, int n_split, const unsigned* w,
                  const float* svh, void* c, float* ws, unsigned* tickets, int K, int N, int SKG, int full,
                  float out_scale, hipStream_t st) {
-  dim3 grid(N / 128, SKG), block(256);
-  if (M == 256)
-    hipLaunchKernelGGL((tq_m256_kernel<KB, 4>), grid, block, 0, st, a0, a1, n_split, w, svh, c, ws, tickets, M,
-                       K, N, SKG, full, out_scale);
-  else
-    hipLaunchKernelGGL((tq_m256_kernel<KB, 2>), grid, block, 0, st, a0, a1, n_split, w, svh, c, ws, tickets, M,
-                       K, N, SKG, full, out_scale);
+  (void)tickets;
+  if (M == 256) m256_launch_rt<KB, 8>(a0, a1, n_split, w, svh, c, ws, M, K, N, SKG, full, out_scale, st);
+  else m256_launch_rt<KB, 4>(a0, a1, n_split, w, svh, c, ws, M, K, N, SKG, full, out_scale, st);
 }
 
 void m256_run(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c, int64_t ws,
