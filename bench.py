@@ -36,7 +36,7 @@ def parse():
     ap.add_argument("--kernel-only", action="store_true", help="only the GEMV launches (for rocprof)")
     ap.add_argument("--no-m256", action="store_true", help="skip the M = 256 prefill GEMM leg")
     ap.add_argument("--no-w4", action="store_true", help="skip the w4a16 LM-head leg")
-    ap.add_argument("--no-i8", action="store_true", help="skip the int8 prefill GEMM leg")
+    ap.add_argument("--no-i8", action="store_true", help="skip the int8 prefill GEMM legs")
     ap.add_argument("--pmc", action="store_true",
                     help="counter pass for rocprofv3 --pmc: a 512 MiB copy (calibration) and two eager "
                          "passes of the GEMV launches; prints no JSON line")
@@ -160,6 +160,7 @@ def main():
     m256 = None if args.no_m256 else bench_m256(api, WL, KB)
     w4 = None if args.no_w4 else bench_w4a16(api, WL)
     i8 = None if args.no_i8 else bench_int8(api, WL)
+    ti8 = None if args.no_i8 else bench_trellis_i8(api, WL, KB)
 
     cpu = None
     if not args.no_cpu:
@@ -191,6 +192,7 @@ def main():
         "m256": m256,
         "w4a16": w4,
         "int8": i8,
+        "trellis_int8": ti8,
         "wall_s": round(wall, 3),
     }
     print(json.dumps(line), flush=True)
@@ -386,6 +388,43 @@ def bench_int8(api, WL, R=4):
         torch.cuda.empty_cache()
     return {"metric": "int8 x int8 prefill GEMM TOP/s (M=256)", "kernel": "i8_gemm_kernel",
             "peak_TOPs": 5000.0, "peak_GBs": HBM_PEAK_GBS, "cases": res}
+
+
+def bench_trellis_i8(api, WL, KB, R=4):
+    """The int8 x int8 TRELLIS prefill GEMM (r4d_gemm_trellis_nt_i8 per-128 scales, _i8c coarse) at the MLP shapes
+    of BASELINE config 4, weights as trellis words (decoded and quantized in the kernel). TOP/s = 2 M K N per
+    launch (back to back over rotating word copies in a HIP graph)."""
+    import numpy as np
+    import torch
+    dev = torch.device("cuda:0")
+    M = 256
+    res = {}
+    for K, N in ((5120, 17408), (17408, 5120)):
+        nw = K * N * KB // 32
+        copies = max(2, int(np.ceil(1.0e9 / (nw * 4))))
+        words = [torch.randint(-2**31, 2**31 - 1, (nw,), dtype=torch.int32, device=dev) for _ in range(copies)]
+        x = torch.from_numpy(WL.activations_f16(M, K, 7, outlier_frac=0.01).view("int16")).to(dev)
+        svh = torch.from_numpy(WL.svh_scales(N, 8)).to(dev)
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        skg = 1 if N > 8192 else 4
+        ws = torch.empty(max(1, skg * M * N), dtype=torch.float32, device=dev)
+        for coarse in (False, True):
+            a8, sa = api.i8_quant(x, blk=not coarse, ref_layout=True)
+            sws = [api.trellis_i8_table(w, K, N, KB, coarse) for w in words]
+
+            def gemm():
+                for w, sw in zip(words, sws):
+                    api.trellis_gemm_i8(a8, sa, w, sw, svh, K, N, KB, coarse=coarse, skg=skg, out=out, ws=ws,
+                                        out_scale=0.08838834764831845)
+            ms = _graph_ms(gemm, R, copies)
+            ops = 2.0 * M * K * N
+            res[f"K{K}_N{N}_{'coarse' if coarse else 'per128'}"] = {
+                "gemm_us": round(ms * 1e3, 2), "TOPs": round(ops / (ms * 1e-3) / 1e12, 1),
+                "frac_int8_peak": round(ops / (ms * 1e-3) / 5.0e15, 4), "skg": skg}
+        del words
+        torch.cuda.empty_cache()
+    return {"metric": "int8 x int8 trellis prefill GEMM TOP/s (M=256, KB4)", "kernel": "ti8_gemm_kernel",
+            "peak_TOPs": 5000.0, "cases": res}
 
 
 def cpu_baseline(KB):

@@ -131,6 +131,30 @@ const char* r4d_gemm_i8_dense_check(int M, int K, int N, int SKG);
 size_t r4d_gemm_i8_dense_ws_bytes(int M, int N, int SKG);
 int r4d_mi355x_i8_skg(int K, int N);
 
+/* ---- int8 x int8 trellis prefill GEMM (r4d.h:456-521) ---------------------------------------- */
+/* r4d.h:490-492: the weight scale table SW [K/128][N] fp32 (s_eff = 1 / rs, rs = f16(min(1 / s, 60000)),
+ * s = max|w| / 127 per (column, 128 k), 1 for an all-zero group) from the pair-grid words, and the int8
+ * weights the GEMM quantizes on the fly (w8: W8 block layout; wp, if not 0: plain [N][K]). */
+size_t r4d_trellis_i8_wscale_count(int K, int N);
+void   r4d_trellis_i8_wscale(int64_t w, int64_t sw, int K, int N, int KB, int64_t stream);
+void   r4d_trellis_i8_dump_w(int64_t w, int64_t sw, int64_t w8, int64_t wp, int K, int N, int KB, int64_t stream);
+/* r4d.h:495-499: C bf16 [256][N] = bf16((FWHT128(sum_kb float(int32(A8 . W8)) * (sa sw)) * svh) * out_scale);
+ * columns >= n_split read a8_1 / sa_1 (a8_1 = 0: a8_0, then n_split = N); ws fp32 ws_bytes(M, N, skg) when
+ * skg > 1 (then a second launch adds the slices); tickets accepted and unused; skw checked, not used. */
+void r4d_gemm_trellis_nt_i8(int64_t a8_0, int64_t sa_0, int64_t a8_1, int64_t sa_1, int n_split, int64_t w,
+                            int64_t sw, int64_t svh, int64_t c, int64_t ws, int64_t tickets, int M, int K, int N,
+                            int KB, int skw, int skg, float out_scale, int64_t stream);
+const char* r4d_gemm_trellis_nt_i8_check(int M, int K, int N, int n_split, int KB, int skw, int skg);
+size_t r4d_gemm_trellis_nt_i8_ws_bytes(int M, int N, int SKG);
+/* r4d.h:514-521: the coarse sibling: SWC [N] (one scale per column over K), SA [256] (per row, from
+ * r4d_trellis_i8_quant_act_row), the int32 sum of the slice scaled once by sa[row] * swc[col]. */
+size_t r4d_trellis_i8_wscale_col_count(int K, int N);
+void   r4d_trellis_i8_wscale_col(int64_t w, int64_t swc, int K, int N, int KB, int64_t stream);
+void   r4d_trellis_i8_dump_w_col(int64_t w, int64_t swc, int64_t w8, int64_t wp, int K, int N, int KB, int64_t stream);
+void r4d_gemm_trellis_nt_i8c(int64_t a8_0, int64_t sa_0, int64_t a8_1, int64_t sa_1, int n_split, int64_t w,
+                             int64_t swc, int64_t svh, int64_t c, int64_t ws, int64_t tickets, int M, int K, int N,
+                             int KB, int skw, int skg, float out_scale, int64_t stream);
+
 /* ---- input transform and FWHT (src/kernels/include/r4dx/kernels/kernels.h) --------------------- */
 /* kernels.h:110-128 r4dx_trellis_input_bf16: out[o][m,k] = f16(FWHT128(fp32(x) * suh[o])[k] * scale),
  * scale = float(2^prescale_log2 / sqrt(128)); x bf16 [M][K]; suh / out: HOST arrays of nout device

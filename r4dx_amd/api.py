@@ -205,3 +205,41 @@ def i8_dense_gemm(a8, sa, w8, sw, K, N, scale_mode=0, skg=None, raw=False, out=N
         L.r4d_gemm_i8_dense(_p(a8), _p(sa), _p(w8), _p(sw), _p(out), _p(work.ws), _p(work.tickets), M, K, N, skg,
                             scale_mode, st)
     return out
+
+
+def trellis_i8_table(w, K, N, KB, coarse=False, stream=None):
+    """The weight scale table: SW [K/128][N] (r4d_trellis_i8_wscale) or SWC [N] (coarse, _wscale_col)."""
+    L = lib()
+    n = L.r4d_trellis_i8_wscale_col_count(K, N) if coarse else L.r4d_trellis_i8_wscale_count(K, N)
+    sw = torch.empty(n, dtype=torch.float32, device=w.device)
+    (L.r4d_trellis_i8_wscale_col if coarse else L.r4d_trellis_i8_wscale)(_p(w), _p(sw), K, N, KB, _stream(stream))
+    return sw
+
+
+def trellis_i8_dump(w, sw, K, N, KB, coarse=False, plain=True, stream=None):
+    """The int8 weights the GEMM quantizes on the fly: (w8 block layout, plain [N][K] or None)."""
+    L = lib()
+    w8 = torch.empty(N * K, dtype=torch.int8, device=w.device)
+    wp = torch.empty((N, K), dtype=torch.int8, device=w.device) if plain else None
+    f = L.r4d_trellis_i8_dump_w_col if coarse else L.r4d_trellis_i8_dump_w
+    f(_p(w), _p(sw), _p(w8), _p(wp) if plain else 0, K, N, KB, _stream(stream))
+    return w8, wp
+
+
+def trellis_gemm_i8(a8, sa, w, sw, svh, K, N, KB, coarse=False, a8_1=None, sa_1=None, n_split=None, skw=2, skg=1,
+                    out=None, ws=None, out_scale=1.0, stream=None):
+    """C bf16 [256][N] = r4d_gemm_trellis_nt_i8 (per-128 scales) or _i8c (coarse)."""
+    L = lib()
+    M = 256
+    n_split = N if n_split is None else n_split
+    msg = L.r4d_gemm_trellis_nt_i8_check(M, K, N, n_split, KB, skw, skg)
+    if msg:
+        raise ValueError(msg.decode())
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a8.device)
+    if ws is None and skg > 1:
+        ws = torch.empty(L.r4d_gemm_trellis_nt_i8_ws_bytes(M, N, skg) // 4, dtype=torch.float32, device=a8.device)
+    f = L.r4d_gemm_trellis_nt_i8c if coarse else L.r4d_gemm_trellis_nt_i8
+    f(_p(a8), _p(sa), _p(a8_1) if a8_1 is not None else 0, _p(sa_1) if sa_1 is not None else 0, n_split, _p(w), _p(sw),
+      _p(svh), _p(out), _p(ws) if ws is not None else 0, 0, M, K, N, KB, skw, skg, out_scale, _stream(stream))
+    return out

@@ -37,6 +37,12 @@ inline bool pow2_in(int v, int lo, int hi) {
 }
 inline std::string str(long long v) { return std::to_string(v); }
 
+// The second pass of a split prefill launch (trellis_m256.hip): ws holds SKG fp32 slices [SKG][M][N];
+// they are added in slice order, then full: FWHT-128 per column group (the reference's stage order), svh,
+// out_scale, one bf16 rounding into C; else the fp32 sums into C. M a multiple of 32, N of 128.
+void launch_split_finish(const float* ws, const float* svh, void* c, int M, int N, int SKG, int full, float out_scale,
+                         hipStream_t st);
+
 }  // namespace r4d
 
 // Arguments of one trellis GEMV launch (trellis_gemv.hip).

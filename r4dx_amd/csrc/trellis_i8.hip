@@ -1,0 +1,526 @@
+// trellis_i8.hip -- the int8 x int8 trellis prefill GEMM on gfx950: r4d_gemm_trellis_nt_i8 (per-128 scales) and
+// r4d_gemm_trellis_nt_i8c (coarse scales), their weight scale tables (r4d_trellis_i8_wscale / _col), the int8 weight
+// dumps (r4d_trellis_i8_dump_w / _col), _check and _ws_bytes: the C ABI of the reference's
+// third_party/libr4d/r4d.h:456-521.
+//
+// C bf16 [256][N] = bf16((FWHT128(sum) * svh) * out_scale) with
+//   per-128: sum = sum_kb float(int32(A8_kb . W8_kb)) * (sa[kb][row] * sw[kb][col])    (fp32, k-block order)
+//   coarse:  sum = float(int32(A8 . W8 over the slice)) * (sa[row] * sw[col])
+// where W8 is the decoded trellis weight Q quantized on the fly: rs = f16(min(1 / s_eff, 60000)) for the
+// table's s_eff = 1 / rs, q = low byte of f16(w * rs + 1536) (one rounding: round(w * rs) lands in the
+// low byte, the f16 spacing at 1536 being 1) -- the reference's rule (r4d_trellis_i8.h:129-151,
+// tests/kernels/int8_gemm_proto_ref.h:57-77). The table: s = max|w| / 127 per (column, 128 k) or per column
+// over K (1 for an all-zero group), rs as above, s_eff = 1 / rs (IEEE fp32).
+//
+// DESIGN (MI355X): v_mfma_i32_16x16x64_i8; a workgroup is 8 waves = 256 rows x one 128-column group x one K
+// slice, in 64-k steps. Wave w owns rows 32 w .. 32 w + 31 (two row tiles of A8's row group w / 2) against
+// all 8 column tiles; its A fragments come straight from the A8 layout (two 8-byte halves per lane, 128
+// contiguous bytes per 16 lanes) through a register ring. B goes through a double-buffered 8 KiB LDS stage
+// [k-tile][column][16 B]: the decode of the next step is shared out -- waves w and w + 4 take turns on tile
+// pair w & 3 -- so every SIMD runs one decode and two waves' MFMAs per step. A decode lane's two fragment
+// halves (element e of half h <-> k = 8 (e >> 2) + 4 h + (e & 3)) quantize, in that order, to exactly the
+// 16 bytes an MFMA lane needs in A8's k order, so nothing is permuted. Unsplit, the FWHT-128 epilogue runs
+// in registers (column bits 0-3 across lanes, 4-6 across column tiles); split K writes fp32 slices to ws
+// and the split finish pass (trellis_m256.hip) adds them in order and runs the same epilogue.
+#include "r4d_dev.h"
+#include "r4d_host.h"
+#include "r4d_mi355x.h"
+
+namespace {
+
+typedef __amdgpu_buffer_rsrc_t r4_rsrc;
+__device__ __forceinline__ r4_rsrc mk_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ r4i4 mfma_i8(r4i4 a, r4i4 b, r4i4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// ---- the weight-side quantizer --------------------------------------------------------------------------
+__device__ __forceinline__ float ti8_scale_from_amax(float amax) { return amax > 0.f ? amax / 127.0f : 1.0f; }
+// rs as the f16 bits, duplicated into both halves; from s (the table builder) or from the table's s_eff
+__device__ __forceinline__ unsigned ti8_rs_from_s(float s) {
+  const _Float16 h = (_Float16)__builtin_fminf(1.0f / s, 60000.f);
+  const unsigned b = __builtin_bit_cast(unsigned short, h);
+  return b | (b << 16);
+}
+// four f16 weights (two dwords, element order) -> four int8 bytes: low byte of f16(w * rs + 1536)
+__device__ __forceinline__ unsigned ti8_q4(unsigned d0, unsigned d1, unsigned rs2) {
+  const r4h2 c = {(_Float16)1536.f, (_Float16)1536.f};
+  const r4h2 x0 = __builtin_elementwise_fma(__builtin_bit_cast(r4h2, d0), __builtin_bit_cast(r4h2, rs2), c);
+  const r4h2 x1 = __builtin_elementwise_fma(__builtin_bit_cast(r4h2, d1), __builtin_bit_cast(r4h2, rs2), c);
+  return __builtin_amdgcn_perm(__builtin_bit_cast(unsigned, x1), __builtin_bit_cast(unsigned, x0), 0x06040200u);
+}
+// max |w| over the lane's 16 values of column slot cs (fp32; exact)
+__device__ __forceinline__ float ti8_amax16(const unsigned (&d)[2][2][4], int cs) {
+  float m = 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const r4h2 v = __builtin_bit_cast(r4h2, d[cs][h][j]);
+      m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fabsf((float)v[0]), __builtin_fabsf((float)v[1])));
+    }
+  return m;
+}
+
+// The decode lane map of one (tile pair, 4 k-tiles) step (the GEMV's): lane q = l >> 4 takes k-tile q, t =
+// (l >> 3) & 1 and c = l & 7 the columns 32 pair + 16 t + 8 cs + c (cs = 0, 1).
+template <int KB>
+struct TileWords {
+  r4_rsrc r;
+  unsigned own, hist;
+  __device__ __forceinline__ TileWords(const unsigned* W, int pair, int KT, int kt0, int ktw, int lane) {
+    constexpr int BLK = 16 * KB;
+    r = mk_rsrc(W + ((size_t)pair * KT + kt0) * BLK, (unsigned)ktw * BLK * 4u);
+    const int q = lane >> 4, t = (lane >> 3) & 1, c = lane & 7;
+    const unsigned tile = (unsigned)(q * 16 * KB + t * 8 * KB);
+    own = (tile + KB * c) * 4u;
+    hist = (tile + (KB * c - 1 + 8 * KB) % (8 * KB)) * 4u;
+  }
+  __device__ __forceinline__ void load(unsigned (&w)[KB + 1], int st) const {
+    const unsigned so = (unsigned)st * (4u * 16u * KB * 4u);
+    if constexpr (KB == 4) {
+      const r4u4 v = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(r, own + so, 0, 0));
+      w[1] = v[0]; w[2] = v[1]; w[3] = v[2]; w[4] = v[3];
+    } else {
+#pragma unroll
+      for (int i = 0; i < KB; ++i) w[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(r, own + so + 4 * i, 0, 0);
+    }
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, hist + so, 0, 0);
+  }
+};
+
+// ---- the scale table: one wave per (tile pair, K range); COL: the range is the whole K ----------------------
+template <int KB, bool COL>
+__global__ __launch_bounds__(64) void ti8_wscale_kernel(const unsigned* __restrict__ W, float* __restrict__ sw, int K,
+                                                        int N) {
+  const int lane = threadIdx.x, pair = blockIdx.x, kb = blockIdx.y;
+  const int KT = K >> 4;
+  const int kt0 = COL ? 0 : kb * 8, ktw = COL ? KT : 8;
+  const TileWords<KB> tw(W, pair, KT, kt0, ktw, lane);
+  float m[2] = {0.f, 0.f};
+  for (int st = 0; st < ktw / 4; ++st) {
+    unsigned w[KB + 1], d[2][2][4];
+    tw.load(w, st);
+    r4_decode<KB>(w, d);
+    m[0] = __builtin_fmaxf(m[0], ti8_amax16(d, 0));
+    m[1] = __builtin_fmaxf(m[1], ti8_amax16(d, 1));
+  }
+#pragma unroll
+  for (int cs = 0; cs < 2; ++cs) {
+    m[cs] = __builtin_fmaxf(m[cs], __shfl_xor(m[cs], 16, 64));
+    m[cs] = __builtin_fmaxf(m[cs], __shfl_xor(m[cs], 32, 64));
+  }
+  if (lane < 16) {
+    const int t = (lane >> 3) & 1, c = lane & 7;
+#pragma unroll
+    for (int cs = 0; cs < 2; ++cs) {
+      const unsigned rs = ti8_rs_from_s(ti8_scale_from_amax(m[cs])) & 0xFFFFu;
+      const float seff = 1.0f / (float)__builtin_bit_cast(_Float16, (unsigned short)rs);
+      sw[(size_t)(COL ? 0 : kb) * N + 32 * pair + 16 * t + 8 * cs + c] = seff;
+    }
+  }
+}
+
+// ---- the int8 weights the GEMM uses: W8 block layout (w8) and, if wp, plain [N][K] --------------------------
+template <int KB, bool COL>
+__global__ __launch_bounds__(64) void ti8_dump_kernel(const unsigned* __restrict__ W, const float* __restrict__ sw,
+                                                      unsigned char* __restrict__ w8, signed char* __restrict__ wp,
+                                                      int K, int N) {
+  const int lane = threadIdx.x, pair = blockIdx.x, st = blockIdx.y;   // one step = 4 k-tiles
+  const int KT = K >> 4;
+  const TileWords<KB> tw(W, pair, KT, 0, KT, lane);
+  unsigned w[KB + 1], d[2][2][4];
+  tw.load(w, st);
+  r4_decode<KB>(w, d);
+  const int q = lane >> 4, t = (lane >> 3) & 1, c = lane & 7;
+  const int kt = 4 * st + q, kb = kt >> 3;
+#pragma unroll
+  for (int cs = 0; cs < 2; ++cs) {
+    const int n = 32 * pair + 16 * t + 8 * cs + c;
+    const unsigned rs2 = ti8_rs_from_s(sw[(size_t)(COL ? 0 : kb) * N + n]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const unsigned lo = ti8_q4(d[cs][h][0], d[cs][h][1], rs2), hi = ti8_q4(d[cs][h][2], d[cs][h][3], rs2);
+      const int L = 16 * h + 8 * t + c;   // r4d_trellis_i8_layout.h:56-64 W8Offset's lane
+      *(r4u2*)(w8 + ((size_t)pair * KT + kt) * 512 + L * 16 + cs * 8) = (r4u2){lo, hi};
+      if (wp) {   // element e <-> k = 8 (e >> 2) + 4 h + (e & 3)
+        *(unsigned*)(wp + (size_t)n * K + 16 * kt + 4 * h) = lo;
+        *(unsigned*)(wp + (size_t)n * K + 16 * kt + 8 + 4 * h) = hi;
+      }
+    }
+  }
+}
+
+// ---- the GEMM ---------------------------------------------------------------------------------------------
+struct TI8Args {
+  const signed char* a8[2];
+  const float* sa[2];
+  int n_split;
+  const unsigned* w;
+  const float* sw;
+  const float* svh;
+  void* c;
+  float* ws;
+  int K, N, SKG;
+  float out_scale;
+};
+
+// the B stage's column slot: bit 3 flipped on odd 16-column tiles (a decode lane writes columns 16 t + 8 cs +
+// c of its pair: the t = 0 and t = 1 lanes of one write then use different banks)
+__device__ __forceinline__ int ti8_bslot(int n) { return n ^ (((n >> 4) & 1) << 3); }
+
+template <int KB, bool P128>
+__global__ __launch_bounds__(512, 1) void ti8_gemm_kernel(TI8Args p) {
+  __shared__ __attribute__((aligned(16))) unsigned char bst[2][4][128][16];   // [stage][k-tile][column slot][16 B]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int group = blockIdx.x, ky = blockIdx.y;
+  const int K = p.K, N = p.N, KT = K >> 4;
+  const int ktw = KT / p.SKG, kt0 = ky * ktw, nst = ktw >> 2;
+  const int n0 = group * 128;
+  const int part = (p.a8[1] != nullptr && n0 >= p.n_split) ? 1 : 0;
+  const int g = lane >> 4, r16 = lane & 15;
+
+  // ---- the decode this wave takes its turn at: pair w & 3, the steps of parity w >> 2
+  const int dpair = group * 4 + (wave & 3), dpar = wave >> 2;
+  const TileWords<KB> tw(p.w, dpair, KT, kt0, ktw, lane);
+  const int dq = lane >> 4, dt = (lane >> 3) & 1, dc = lane & 7;
+  // rs of the decode lane's two columns: coarse -- fixed for the launch; per-128 -- from the ring's s_eff
+  unsigned rsc[2] = {0u, 0u};
+  if constexpr (!P128) {
+#pragma unroll
+    for (int cs = 0; cs < 2; ++cs) rsc[cs] = ti8_rs_from_s(p.sw[n0 + 32 * (wave & 3) + 16 * dt + 8 * cs + dc]);
+  }
+  auto put = [&](const unsigned (&w)[KB + 1], const float (&dsw)[2], int st) {
+    unsigned d[2][2][4];
+    r4_decode<KB>(w, d);
+#pragma unroll
+    for (int cs = 0; cs < 2; ++cs) {
+      const int nl = 32 * (wave & 3) + 16 * dt + 8 * cs + dc;
+      const unsigned rs2 = P128 ? ti8_rs_from_s(dsw[cs]) : rsc[cs];
+      const r4u4 v = {ti8_q4(d[cs][0][0], d[cs][0][1], rs2), ti8_q4(d[cs][0][2], d[cs][0][3], rs2),
+                      ti8_q4(d[cs][1][0], d[cs][1][1], rs2), ti8_q4(d[cs][1][2], d[cs][1][3], rs2)};
+      *(r4u4*)&bst[st & 1][dq][ti8_bslot(nl)][0] = v;
+    }
+  };
+  // the table entries of the decode lane's columns for step st
+  auto load_dsw = [&](float (&dsw)[2], int st) {
+    if constexpr (P128) {
+      const int kb = (kt0 + 4 * st) >> 3;
+#pragma unroll
+      for (int cs = 0; cs < 2; ++cs) dsw[cs] = p.sw[(size_t)kb * N + n0 + 32 * (wave & 3) + 16 * dt + 8 * cs + dc];
+    } else {
+      dsw[0] = dsw[1] = 0.f;
+    }
+  };
+
+  // ---- this wave's A: rows 32 w + 16 ii + r16 = row group rg, row tiles i0, i0 + 1
+  const int rg = wave >> 1, i0 = 2 * (wave & 1);
+  const r4_rsrc ar = mk_rsrc(p.a8[part], 256u * (unsigned)K);
+  const unsigned abase = ((unsigned)(rg * KT + kt0 + g) * 4u + (unsigned)i0) * 256u + (unsigned)r16 * 8u;
+  const float* SA = p.sa[part];
+  struct St {
+    r4u2 a[2][2];
+    unsigned w[KB + 1];   // the words of step st + 1 (what this wave decodes after step st's barrier)
+    float dsw[2];         // per-128: their columns' s_eff
+    r4f4 sa[2];           // per-128, odd steps: sa[kb][rows of the two row tiles]
+    float sw[8];          // per-128, odd steps: sw[kb][column of each column tile]
+  };
+  auto load = [&](St& s, int st, bool odd) {
+    const int sc = min(st, nst - 1);
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        s.a[ii][h] = __builtin_bit_cast(
+            r4u2, __builtin_amdgcn_raw_buffer_load_b64(ar, abase + (unsigned)sc * 4096u + ii * 256u + h * 128u, 0, 0));
+    const int nx = min(sc + 1, nst - 1);
+    tw.load(s.w, nx);
+    load_dsw(s.dsw, nx);
+    if constexpr (P128) {
+      if (odd) {
+        const int kb = (kt0 + 4 * sc) >> 3;
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) s.sa[ii] = *(const r4f4*)(SA + (size_t)kb * 256 + 32 * wave + 16 * ii + 4 * g);
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct) s.sw[ct] = p.sw[(size_t)kb * N + n0 + 16 * ct + r16];
+      }
+    }
+  };
+
+  r4i4 iacc[2][8];
+  r4f4 facc[P128 ? 2 : 1][8];
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct) {
+      iacc[ii][ct] = (r4i4){0, 0, 0, 0};
+      if constexpr (P128) facc[ii][ct] = (r4f4){0.f, 0.f, 0.f, 0.f};
+    }
+
+  auto step = [&](const St& s, int st, bool odd) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();                 // stage st landed; stage st + 1 free
+    if (st + 1 < nst && ((st + 1) & 1) == dpar) put(s.w, s.dsw, st + 1);
+    const unsigned char* stg = &bst[st & 1][g][0][0];
+    r4i4 a[2];
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+      a[ii] = (r4i4){(int)s.a[ii][0].x, (int)s.a[ii][0].y, (int)s.a[ii][1].x, (int)s.a[ii][1].y};
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct) {
+      const r4i4 b = *(const r4i4*)(stg + ti8_bslot(16 * ct + r16) * 16);
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) iacc[ii][ct] = mfma_i8(a[ii], b, iacc[ii][ct]);
+    }
+    if constexpr (P128) {
+      if (odd) {   // the 128-k block is complete: acc += float(int32) * (sa[row] * sw[col])
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              facc[ii][ct][j] = __builtin_fmaf((float)iacc[ii][ct][j], s.sa[ii][j] * s.sw[ct], facc[ii][ct][j]);
+              iacc[ii][ct][j] = 0;
+            }
+        }
+      }
+    }
+  };
+
+  // prologue: the waves of parity 0 decode step 0 into stage 0 before the first barrier
+  {
+    unsigned w0[KB + 1];
+    float d0[2];
+    tw.load(w0, 0);
+    load_dsw(d0, 0);
+    if (dpar == 0 && nst > 0) put(w0, d0, 0);
+  }
+  // statically indexed ring; PF even, so slot i always carries steps of parity i (a 128-k block = 2 steps)
+  constexpr int PF = 2;
+  St ring[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) load(ring[i], i, (i & 1) != 0);
+  int st = 0;
+  for (; st + PF <= nst; st += PF) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      step(ring[i], st + i, (i & 1) != 0);
+      load(ring[i], st + i + PF, (i & 1) != 0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PF - 1; ++i)
+    if (st + i < nst) step(ring[i], st + i, (i & 1) != 0);
+
+  // this slice's values: rows 32 w + 16 ii + 4 g + j, column n0 + 16 ct + r16
+  float v[2][8][4];
+  if constexpr (P128) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[ii][ct][j] = facc[ii][ct][j];
+  } else {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const r4f4 sav = *(const r4f4*)(SA + 32 * wave + 16 * ii + 4 * g);
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct) {
+        const float swc = p.sw[n0 + 16 * ct + r16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[ii][ct][j] = (float)iacc[ii][ct][j] * (sav[j] * swc);
+      }
+    }
+  }
+  if (p.SKG > 1) {
+    float* dst = p.ws + (size_t)ky * 256 * N;
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct) dst[(size_t)(32 * wave + 16 * ii + 4 * g + j) * N + n0 + 16 * ct + r16] = v[ii][ct][j];
+    return;
+  }
+  // FWHT-128 over the group's columns, stages lg = 0..6 in order (the lower index keeps a + b, the upper
+  // takes a - b): bits 0-3 are lane bits 0-3, bits 4-6 the column tile ct
+  unsigned short* C = (unsigned short*)p.c;
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float x[8];
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct) x[ct] = v[ii][ct][j];
+#pragma unroll
+      for (int mask = 1; mask <= 8; mask <<= 1) {
+        const bool upper = (lane & mask) != 0;
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct) {
+          const float o = __shfl_xor(x[ct], mask, 64);
+          x[ct] = upper ? o - x[ct] : x[ct] + o;
+        }
+      }
+#pragma unroll
+      for (int b = 1; b <= 4; b <<= 1)
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct)
+          if ((ct & b) == 0) {
+            const float a0 = x[ct], b0 = x[ct | b];
+            x[ct] = a0 + b0;
+            x[ct | b] = a0 - b0;
+          }
+      const int r = 32 * wave + 16 * ii + 4 * g + j;
+#pragma unroll
+      for (int ct = 0; ct < 8; ++ct) {
+        const int n = n0 + 16 * ct + r16;
+        C[(size_t)r * N + n] = r4_bf16_rn((x[ct] * p.svh[n]) * p.out_scale);
+      }
+    }
+}
+
+std::string ti8_check(int M, int K, int N, int n_split, int KB, int skw, int skg) {
+  using r4d::str;
+  if (M != 256) return "M must be 256";
+  if (K <= 0 || N <= 0 || K % 128 || N % 128) return "K and N must be positive multiples of 128";
+  if (n_split < 0 || n_split > N || n_split % 128) return "n_split must be in 0..N and a multiple of 128";
+  if (KB != 4 && KB != 5) return "KB " + str(KB) + " is not instantiated (4, 5)";
+  if (skw != 2 && skw != 4 && skw != 8) return "skw must be 2, 4 or 8";
+  if (skg != 1 && skg != 2 && skg != 4 && skg != 8) return "skg must be 1, 2, 4 or 8";
+  if ((K / 128) % (skw * skg)) return "(K / 128) must be divisible by skw * skg";
+  if ((long long)256 * K >= (1LL << 32)) return "256 K must be below 2^32 bytes";
+  return "";
+}
+
+template <int KB, bool P128>
+void ti8_launch(const TI8Args& a, int N, int SKG, hipStream_t st) {
+  hipLaunchKernelGGL((ti8_gemm_kernel<KB, P128>), dim3(N / 128, SKG), dim3(512), 0, st, a);
+}
+
+void ti8_run(bool p128, int64_t a8_0, int64_t sa_0, int64_t a8_1, int64_t sa_1, int n_split, int64_t w, int64_t sw,
+             int64_t svh, int64_t c, int64_t ws, int64_t tickets, int M, int K, int N, int KB, int skw, int skg,
+             float out_scale, int64_t stream, const char* entry) {
+  (void)tickets;
+  r4d::require(entry, ti8_check(M, K, N, n_split, KB, skw, skg));
+  if (!a8_0 || !sa_0 || !w || !sw || !svh || !c) r4d::fail(entry, "null A8, SA, W, SW, svh or C");
+  if (a8_1 && !sa_1) r4d::fail(entry, "a8_1 without sa_1");
+  if (!a8_1 && n_split != N) r4d::fail(entry, "a one-part launch (a8_1 = 0) needs n_split = N");
+  if (skg > 1 && !ws) r4d::fail(entry, "skg > 1 needs ws");
+  TI8Args a{};
+  a.a8[0] = (const signed char*)a8_0;
+  a.a8[1] = (const signed char*)a8_1;
+  a.sa[0] = (const float*)sa_0;
+  a.sa[1] = a8_1 ? (const float*)sa_1 : (const float*)sa_0;
+  a.n_split = n_split;
+  a.w = (const unsigned*)w;
+  a.sw = (const float*)sw;
+  a.svh = (const float*)svh;
+  a.c = (void*)c;
+  a.ws = (float*)ws;
+  a.K = K;
+  a.N = N;
+  a.SKG = skg;
+  a.out_scale = out_scale;
+  hipStream_t st = (hipStream_t)stream;
+  if (KB == 4) {
+    if (p128) ti8_launch<4, true>(a, N, skg, st); else ti8_launch<4, false>(a, N, skg, st);
+  } else {
+    if (p128) ti8_launch<5, true>(a, N, skg, st); else ti8_launch<5, false>(a, N, skg, st);
+  }
+  if (skg > 1) r4d::launch_split_finish(a.ws, a.svh, a.c, M, N, skg, 1, out_scale, st);
+  r4d::launch_ok(entry);
+}
+
+void ti8_table(bool col, int64_t w, int64_t sw, int K, int N, int KB, int64_t stream, const char* entry) {
+  if (K <= 0 || N <= 0 || K % 128 || N % 128) r4d::fail(entry, "K and N must be positive multiples of 128");
+  if (KB != 4 && KB != 5) r4d::fail(entry, "KB must be 4 or 5");
+  if (!w || !sw) r4d::fail(entry, "null buffer");
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid(N / 32, col ? 1 : K / 128);
+  auto W = (const unsigned*)w;
+  auto S = (float*)sw;
+  if (KB == 4) {
+    if (col) hipLaunchKernelGGL((ti8_wscale_kernel<4, true>), grid, dim3(64), 0, st, W, S, K, N);
+    else hipLaunchKernelGGL((ti8_wscale_kernel<4, false>), grid, dim3(64), 0, st, W, S, K, N);
+  } else {
+    if (col) hipLaunchKernelGGL((ti8_wscale_kernel<5, true>), grid, dim3(64), 0, st, W, S, K, N);
+    else hipLaunchKernelGGL((ti8_wscale_kernel<5, false>), grid, dim3(64), 0, st, W, S, K, N);
+  }
+  r4d::launch_ok(entry);
+}
+
+void ti8_dump(bool col, int64_t w, int64_t sw, int64_t w8, int64_t wp, int K, int N, int KB, int64_t stream,
+              const char* entry) {
+  if (K <= 0 || N <= 0 || K % 128 || N % 128) r4d::fail(entry, "K and N must be positive multiples of 128");
+  if (KB != 4 && KB != 5) r4d::fail(entry, "KB must be 4 or 5");
+  if (!w || !sw || !w8) r4d::fail(entry, "null buffer");
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid(N / 32, K / 64);
+  auto W = (const unsigned*)w;
+  auto S = (const float*)sw;
+  auto B = (unsigned char*)w8;
+  auto P = (signed char*)wp;
+  if (KB == 4) {
+    if (col) hipLaunchKernelGGL((ti8_dump_kernel<4, true>), grid, dim3(64), 0, st, W, S, B, P, K, N);
+    else hipLaunchKernelGGL((ti8_dump_kernel<4, false>), grid, dim3(64), 0, st, W, S, B, P, K, N);
+  } else {
+    if (col) hipLaunchKernelGGL((ti8_dump_kernel<5, true>), grid, dim3(64), 0, st, W, S, B, P, K, N);
+    else hipLaunchKernelGGL((ti8_dump_kernel<5, false>), grid, dim3(64), 0, st, W, S, B, P, K, N);
+  }
+  r4d::launch_ok(entry);
+}
+
+}  // namespace
+
+extern "C" {
+
+// r4d.h:490 (K / 128) N floats
+size_t r4d_trellis_i8_wscale_count(int K, int N) { return (size_t)(K / 128) * (size_t)N; }
+// r4d.h:491
+void r4d_trellis_i8_wscale(int64_t w, int64_t sw, int K, int N, int KB, int64_t stream) {
+  ti8_table(false, w, sw, K, N, KB, stream, "trellis_i8_wscale");
+}
+// r4d.h:492
+void r4d_trellis_i8_dump_w(int64_t w, int64_t sw, int64_t w8, int64_t wp, int K, int N, int KB, int64_t stream) {
+  ti8_dump(false, w, sw, w8, wp, K, N, KB, stream, "trellis_i8_dump_w");
+}
+// r4d.h:495-497; skw is the reference's per-workgroup K split: checked for legality, not used
+void r4d_gemm_trellis_nt_i8(int64_t a8_0, int64_t sa_0, int64_t a8_1, int64_t sa_1, int n_split, int64_t w,
+                            int64_t sw, int64_t svh, int64_t c, int64_t ws, int64_t tickets, int M, int K, int N,
+                            int KB, int skw, int skg, float out_scale, int64_t stream) {
+  ti8_run(true, a8_0, sa_0, a8_1, sa_1, n_split, w, sw, svh, c, ws, tickets, M, K, N, KB, skw, skg, out_scale, stream,
+          "gemm_trellis_nt_i8");
+}
+// r4d.h:498
+const char* r4d_gemm_trellis_nt_i8_check(int M, int K, int N, int n_split, int KB, int skw, int skg) {
+  return r4d::check_result(ti8_check(M, K, N, n_split, KB, skw, skg));
+}
+// r4d.h:499 SKG M N fp32
+size_t r4d_gemm_trellis_nt_i8_ws_bytes(int M, int N, int SKG) { return (size_t)SKG * M * N * 4; }
+// r4d.h:514
+size_t r4d_trellis_i8_wscale_col_count(int K, int N) {
+  (void)K;
+  return (size_t)N;
+}
+// r4d.h:515
+void r4d_trellis_i8_wscale_col(int64_t w, int64_t swc, int K, int N, int KB, int64_t stream) {
+  ti8_table(true, w, swc, K, N, KB, stream, "trellis_i8_wscale_col");
+}
+// r4d.h:516
+void r4d_trellis_i8_dump_w_col(int64_t w, int64_t swc, int64_t w8, int64_t wp, int K, int N, int KB, int64_t stream) {
+  ti8_dump(true, w, swc, w8, wp, K, N, KB, stream, "trellis_i8_dump_w_col");
+}
+// r4d.h:519-521
+void r4d_gemm_trellis_nt_i8c(int64_t a8_0, int64_t sa_0, int64_t a8_1, int64_t sa_1, int n_split, int64_t w,
+                             int64_t swc, int64_t svh, int64_t c, int64_t ws, int64_t tickets, int M, int K, int N,
+                             int KB, int skw, int skg, float out_scale, int64_t stream) {
+  ti8_run(false, a8_0, sa_0, a8_1, sa_1, n_split, w, swc, svh, c, ws, tickets, M, K, N, KB, skw, skg, out_scale,
+          stream, "gemm_trellis_nt_i8c");
+}
+
+}  // extern "C"

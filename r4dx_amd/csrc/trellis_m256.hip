@@ -350,13 +350,16 @@ void m256_run(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64
   if (KB == 4) m256_launch<4>(M, A0, A1, n_split, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, st);
   else if (KB == 5) m256_launch<5>(M, A0, A1, n_split, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, st);
   else m256_launch<3>(M, A0, A1, n_split, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, st);
-  if (SKG > 1)
-    hipLaunchKernelGGL(tq_m256_finish, dim3(N / 128, M / 32), dim3(256), 0, st, (const float*)WS, S, (void*)c, M, N,
-                       SKG, full, out_scale);
+  if (SKG > 1) r4d::launch_split_finish(WS, S, (void*)c, M, N, SKG, full, out_scale, st);
   r4d::launch_ok(entry);
 }
 
 }  // namespace
+
+void r4d::launch_split_finish(const float* ws, const float* svh, void* c, int M, int N, int SKG, int full,
+                              float out_scale, hipStream_t st) {
+  hipLaunchKernelGGL(tq_m256_finish, dim3(N / 128, M / 32), dim3(256), 0, st, ws, svh, c, M, N, SKG, full, out_scale);
+}
 
 extern "C" {
 

@@ -48,6 +48,16 @@ SIGS = {
     "r4d_gemm_i8_dense_check": (CSTR, [I32] * 4),
     "r4d_gemm_i8_dense_ws_bytes": (SZ, [I32] * 3),
     "r4d_mi355x_i8_skg": (I32, [I32, I32]),
+    "r4d_trellis_i8_wscale_count": (SZ, [I32, I32]),
+    "r4d_trellis_i8_wscale": (None, [I64, I64, I32, I32, I32, I64]),
+    "r4d_trellis_i8_dump_w": (None, [I64, I64, I64, I64, I32, I32, I32, I64]),
+    "r4d_gemm_trellis_nt_i8": (None, [I64, I64, I64, I64, I32] + [I64] * 6 + [I32] * 6 + [F32, I64]),
+    "r4d_gemm_trellis_nt_i8_check": (CSTR, [I32] * 7),
+    "r4d_gemm_trellis_nt_i8_ws_bytes": (SZ, [I32] * 3),
+    "r4d_trellis_i8_wscale_col_count": (SZ, [I32, I32]),
+    "r4d_trellis_i8_wscale_col": (None, [I64, I64, I32, I32, I32, I64]),
+    "r4d_trellis_i8_dump_w_col": (None, [I64, I64, I64, I64, I32, I32, I32, I64]),
+    "r4d_gemm_trellis_nt_i8c": (None, [I64, I64, I64, I64, I32] + [I64] * 6 + [I32] * 6 + [F32, I64]),
     "r4dx_trellis_input_bf16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
     "r4dx_trellis_input_f16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
     "r4dx_fwht128_f32": (None, [I64, I64, I32, I64]),
