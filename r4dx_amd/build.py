@@ -18,9 +18,9 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=o
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I" + CSRC, "-I" + os.path.join(ROOT, "include"), "-Wall", "-Wno-unused-function"]
 
-# Per-source extra flags. int8.hip: the MFMA accumulators stay in VGPRs (the AGPR form of the int8 MFMA
+# Per-source extra flags. trellis_i8.hip: the int8 MFMA accumulators stay in VGPRs (the AGPR form of the int8 MFMA
 # does not tie its destination to srcC, and the allocator then rotates 128 accumulators through copies).
-EXTRA = {"int8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
+EXTRA = {"trellis_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
 
 
 def sources():

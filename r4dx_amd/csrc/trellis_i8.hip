@@ -154,11 +154,19 @@ __global__ __launch_bounds__(64) void ti8_dump_kernel(const unsigned* __restrict
 }
 
 // ---- the GEMM ---------------------------------------------------------------------------------------------
+// SC: the scale mode. kSCoarse -- one int32 sum per slice, times sa[row] * sw[col] once; kSABlk -- per 128-k
+// block acc += float(int32) * sa[kb][row], times sw[col] at the end (the dense per-128 activation variant);
+// kSBlk -- per block acc += float(int32) * (sa[kb][row] * sw[kb][col]) (the trellis per-128 mode).
+// OUT: kOutBf16 -- FWHT-128, svh, out_scale, bf16 (the trellis entries); kOutF16 -- plain f16; kOutI32 -- the
+// exact int32 sums (test entry). DENSE: B is int8 in the W8 block layout instead of trellis words.
+constexpr int kSCoarse = 0, kSABlk = 1, kSBlk = 2;
+constexpr int kOutBf16 = 0, kOutF16 = 1, kOutI32 = 2;
+
 struct TI8Args {
   const signed char* a8[2];
   const float* sa[2];
   int n_split;
-  const unsigned* w;
+  const void* w;        // trellis words or W8 bytes
   const float* sw;
   const float* svh;
   void* c;
@@ -171,8 +179,9 @@ struct TI8Args {
 // c of its pair: the t = 0 and t = 1 lanes of one write then use different banks)
 __device__ __forceinline__ int ti8_bslot(int n) { return n ^ (((n >> 4) & 1) << 3); }
 
-template <int KB, bool P128>
+template <int KB, int SC, int OUT, bool DENSE>
 __global__ __launch_bounds__(512, 1) void ti8_gemm_kernel(TI8Args p) {
+  constexpr bool BLKA = SC != kSCoarse;           // per-128 activation scales: fp32 accumulators
   __shared__ __attribute__((aligned(16))) unsigned char bst[2][4][128][16];   // [stage][k-tile][column slot][16 B]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -183,36 +192,50 @@ __global__ __launch_bounds__(512, 1) void ti8_gemm_kernel(TI8Args p) {
   const int part = (p.a8[1] != nullptr && n0 >= p.n_split) ? 1 : 0;
   const int g = lane >> 4, r16 = lane & 15;
 
-  // ---- the decode this wave takes its turn at: pair w & 3, the steps of parity w >> 2
+  // ---- B. Trellis: waves w and w + 4 take turns (steps of parity w >> 2) at decoding pair w & 3. Dense: every
+  // wave copies its 1 KiB of the step's W8 blocks -- pair w >> 1, k-tiles 2 (w & 1) + (lane >> 5) -- every step.
   const int dpair = group * 4 + (wave & 3), dpar = wave >> 2;
-  const TileWords<KB> tw(p.w, dpair, KT, kt0, ktw, lane);
+  const TileWords<KB> tw((const unsigned*)p.w, dpair, KT, kt0, ktw, lane);
   const int dq = lane >> 4, dt = (lane >> 3) & 1, dc = lane & 7;
+  const r4_rsrc wr8 = mk_rsrc(p.w, (unsigned)N * (unsigned)K);
+  const int wpp = wave >> 1, wkt = 2 * (wave & 1) + (lane >> 5), wL = lane & 31;
+  const unsigned w8base = ((unsigned)((group * 4 + wpp) * KT + kt0 + wkt)) * 512u + (unsigned)wL * 16u;
   // rs of the decode lane's two columns: coarse -- fixed for the launch; per-128 -- from the ring's s_eff
   unsigned rsc[2] = {0u, 0u};
-  if constexpr (!P128) {
+  if constexpr (!DENSE && SC != kSBlk) {
 #pragma unroll
     for (int cs = 0; cs < 2; ++cs) rsc[cs] = ti8_rs_from_s(p.sw[n0 + 32 * (wave & 3) + 16 * dt + 8 * cs + dc]);
   }
-  auto put = [&](const unsigned (&w)[KB + 1], const float (&dsw)[2], int st) {
-    unsigned d[2][2][4];
-    r4_decode<KB>(w, d);
+  auto put = [&](const unsigned (&w)[KB + 1], const float (&dsw)[2], const r4u4& wb, int st) {
+    if constexpr (DENSE) {
+      // W8 lane L = 16 h + 8 t + c holds fragment F0 then F1: columns 32 pair + 16 t + 8 F + c, k-half h
+      const int h = wL >> 4, t = (wL >> 3) & 1, c = wL & 7;
+      const int nl = 32 * wpp + 16 * t + c;
+      *(r4u2*)&bst[st & 1][wkt][ti8_bslot(nl)][8 * h] = (r4u2){wb[0], wb[1]};
+      *(r4u2*)&bst[st & 1][wkt][ti8_bslot(nl + 8)][8 * h] = (r4u2){wb[2], wb[3]};
+    } else {
+      unsigned d[2][2][4];
+      r4_decode<KB>(w, d);
 #pragma unroll
-    for (int cs = 0; cs < 2; ++cs) {
-      const int nl = 32 * (wave & 3) + 16 * dt + 8 * cs + dc;
-      const unsigned rs2 = P128 ? ti8_rs_from_s(dsw[cs]) : rsc[cs];
-      const r4u4 v = {ti8_q4(d[cs][0][0], d[cs][0][1], rs2), ti8_q4(d[cs][0][2], d[cs][0][3], rs2),
-                      ti8_q4(d[cs][1][0], d[cs][1][1], rs2), ti8_q4(d[cs][1][2], d[cs][1][3], rs2)};
-      *(r4u4*)&bst[st & 1][dq][ti8_bslot(nl)][0] = v;
+      for (int cs = 0; cs < 2; ++cs) {
+        const int nl = 32 * (wave & 3) + 16 * dt + 8 * cs + dc;
+        const unsigned rs2 = SC == kSBlk ? ti8_rs_from_s(dsw[cs]) : rsc[cs];
+        const r4u4 v = {ti8_q4(d[cs][0][0], d[cs][0][1], rs2), ti8_q4(d[cs][0][2], d[cs][0][3], rs2),
+                        ti8_q4(d[cs][1][0], d[cs][1][1], rs2), ti8_q4(d[cs][1][2], d[cs][1][3], rs2)};
+        *(r4u4*)&bst[st & 1][dq][ti8_bslot(nl)][0] = v;
+      }
     }
   };
-  // the table entries of the decode lane's columns for step st
-  auto load_dsw = [&](float (&dsw)[2], int st) {
-    if constexpr (P128) {
-      const int kb = (kt0 + 4 * st) >> 3;
-#pragma unroll
-      for (int cs = 0; cs < 2; ++cs) dsw[cs] = p.sw[(size_t)kb * N + n0 + 32 * (wave & 3) + 16 * dt + 8 * cs + dc];
+  auto load_b = [&](unsigned (&w)[KB + 1], float (&dsw)[2], r4u4& wb, int st) {
+    if constexpr (DENSE) {
+      wb = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(wr8, w8base + (unsigned)st * 2048u, 0, 0));
     } else {
-      dsw[0] = dsw[1] = 0.f;
+      tw.load(w, st);
+      if constexpr (SC == kSBlk) {
+        const int kb = (kt0 + 4 * st) >> 3;
+#pragma unroll
+        for (int cs = 0; cs < 2; ++cs) dsw[cs] = p.sw[(size_t)kb * N + n0 + 32 * (wave & 3) + 16 * dt + 8 * cs + dc];
+      }
     }
   };
 
@@ -223,10 +246,11 @@ __global__ __launch_bounds__(512, 1) void ti8_gemm_kernel(TI8Args p) {
   const float* SA = p.sa[part];
   struct St {
     r4u2 a[2][2];
-    unsigned w[KB + 1];   // the words of step st + 1 (what this wave decodes after step st's barrier)
-    float dsw[2];         // per-128: their columns' s_eff
+    unsigned w[KB + 1];   // trellis: the words of step st + 1 (what this wave decodes after step st's barrier)
+    float dsw[2];         // trellis per-128: their columns' s_eff
+    r4u4 wb;              // dense: this wave's W8 bytes of step st + 1
     r4f4 sa[2];           // per-128, odd steps: sa[kb][rows of the two row tiles]
-    float sw[8];          // per-128, odd steps: sw[kb][column of each column tile]
+    float sw[8];          // kSBlk, odd steps: sw[kb][column of each column tile]
   };
   auto load = [&](St& s, int st, bool odd) {
     const int sc = min(st, nst - 1);
@@ -236,34 +260,34 @@ __global__ __launch_bounds__(512, 1) void ti8_gemm_kernel(TI8Args p) {
       for (int h = 0; h < 2; ++h)
         s.a[ii][h] = __builtin_bit_cast(
             r4u2, __builtin_amdgcn_raw_buffer_load_b64(ar, abase + (unsigned)sc * 4096u + ii * 256u + h * 128u, 0, 0));
-    const int nx = min(sc + 1, nst - 1);
-    tw.load(s.w, nx);
-    load_dsw(s.dsw, nx);
-    if constexpr (P128) {
+    load_b(s.w, s.dsw, s.wb, min(sc + 1, nst - 1));
+    if constexpr (BLKA) {
       if (odd) {
         const int kb = (kt0 + 4 * sc) >> 3;
 #pragma unroll
         for (int ii = 0; ii < 2; ++ii) s.sa[ii] = *(const r4f4*)(SA + (size_t)kb * 256 + 32 * wave + 16 * ii + 4 * g);
+        if constexpr (SC == kSBlk) {
 #pragma unroll
-        for (int ct = 0; ct < 8; ++ct) s.sw[ct] = p.sw[(size_t)kb * N + n0 + 16 * ct + r16];
+          for (int ct = 0; ct < 8; ++ct) s.sw[ct] = p.sw[(size_t)kb * N + n0 + 16 * ct + r16];
+        }
       }
     }
   };
 
   r4i4 iacc[2][8];
-  r4f4 facc[P128 ? 2 : 1][8];
+  r4f4 facc[BLKA ? 2 : 1][8];
 #pragma unroll
   for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
     for (int ct = 0; ct < 8; ++ct) {
       iacc[ii][ct] = (r4i4){0, 0, 0, 0};
-      if constexpr (P128) facc[ii][ct] = (r4f4){0.f, 0.f, 0.f, 0.f};
+      if constexpr (BLKA) facc[ii][ct] = (r4f4){0.f, 0.f, 0.f, 0.f};
     }
 
   auto step = [&](const St& s, int st, bool odd) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();                 // stage st landed; stage st + 1 free
-    if (st + 1 < nst && ((st + 1) & 1) == dpar) put(s.w, s.dsw, st + 1);
+    if (st + 1 < nst && (DENSE || ((st + 1) & 1) == dpar)) put(s.w, s.dsw, s.wb, st + 1);
     const unsigned char* stg = &bst[st & 1][g][0][0];
     r4i4 a[2];
 #pragma unroll
@@ -275,32 +299,33 @@ __global__ __launch_bounds__(512, 1) void ti8_gemm_kernel(TI8Args p) {
 #pragma unroll
       for (int ii = 0; ii < 2; ++ii) iacc[ii][ct] = mfma_i8(a[ii], b, iacc[ii][ct]);
     }
-    if constexpr (P128) {
-      if (odd) {   // the 128-k block is complete: acc += float(int32) * (sa[row] * sw[col])
+    if constexpr (BLKA) {
+      if (odd) {   // the 128-k block is complete: acc += float(int32) * scale
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii) {
+        for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
           for (int ct = 0; ct < 8; ++ct)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              facc[ii][ct][j] = __builtin_fmaf((float)iacc[ii][ct][j], s.sa[ii][j] * s.sw[ct], facc[ii][ct][j]);
+              const float sc = SC == kSBlk ? s.sa[ii][j] * s.sw[ct] : s.sa[ii][j];
+              facc[ii][ct][j] = __builtin_fmaf((float)iacc[ii][ct][j], sc, facc[ii][ct][j]);
               iacc[ii][ct][j] = 0;
             }
-        }
       }
     }
   };
 
-  // prologue: the waves of parity 0 decode step 0 into stage 0 before the first barrier
+  // prologue: the waves that stage step 0 do so before the first barrier
   {
     unsigned w0[KB + 1];
-    float d0[2];
-    tw.load(w0, 0);
-    load_dsw(d0, 0);
-    if (dpar == 0 && nst > 0) put(w0, d0, 0);
+    float d0[2] = {0.f, 0.f};
+    r4u4 b0 = {0u, 0u, 0u, 0u};
+    load_b(w0, d0, b0, 0);
+    if (nst > 0 && (DENSE || dpar == 0)) put(w0, d0, b0, 0);
   }
-  // statically indexed ring; PF even, so slot i always carries steps of parity i (a 128-k block = 2 steps)
-  constexpr int PF = 2;
+  // statically indexed ring; PF even, so slot i always carries steps of parity i (a 128-k block = 2 steps);
+  // deeper where the registers allow (the per-128 modes hold fp32 and int32 accumulators)
+  constexpr int PF = BLKA ? 2 : 4;
   St ring[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) load(ring[i], i, (i & 1) != 0);
@@ -316,72 +341,124 @@ __global__ __launch_bounds__(512, 1) void ti8_gemm_kernel(TI8Args p) {
   for (int i = 0; i < PF - 1; ++i)
     if (st + i < nst) step(ring[i], st + i, (i & 1) != 0);
 
-  // this slice's values: rows 32 w + 16 ii + 4 g + j, column n0 + 16 ct + r16
-  float v[2][8][4];
-  if constexpr (P128) {
+  // ---- this slice's values: rows 32 w + 16 ii + 4 g + j, column n0 + 16 ct + r16
+  if constexpr (OUT == kOutI32) {
+    if (p.SKG > 1) {
+      int* dst = (int*)p.ws + (size_t)ky * 256 * N;
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii)
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct)
+            dst[(size_t)(32 * wave + 16 * ii + 4 * g + j) * N + n0 + 16 * ct + r16] = iacc[ii][ct][j];
+    } else {
+      int* C = (int*)p.c;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct)
+            C[(size_t)(32 * wave + 16 * ii + 4 * g + j) * N + n0 + 16 * ct + r16] = iacc[ii][ct][j];
+    }
+    return;
+  } else {
+    float v[2][8][4];
+    float swc[8];
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct) swc[ct] = SC == kSBlk ? 1.f : p.sw[n0 + 16 * ct + r16];
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      r4f4 sav = (r4f4){1.f, 1.f, 1.f, 1.f};
+      if constexpr (SC == kSCoarse) sav = *(const r4f4*)(SA + 32 * wave + 16 * ii + 4 * g);
 #pragma unroll
       for (int ct = 0; ct < 8; ++ct)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[ii][ct][j] = facc[ii][ct][j];
-  } else {
-#pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-      const r4f4 sav = *(const r4f4*)(SA + 32 * wave + 16 * ii + 4 * g);
-#pragma unroll
-      for (int ct = 0; ct < 8; ++ct) {
-        const float swc = p.sw[n0 + 16 * ct + r16];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[ii][ct][j] = (float)iacc[ii][ct][j] * (sav[j] * swc);
-      }
-    }
-  }
-  if (p.SKG > 1) {
-    float* dst = p.ws + (size_t)ky * 256 * N;
-#pragma unroll
-    for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int ct = 0; ct < 8; ++ct) dst[(size_t)(32 * wave + 16 * ii + 4 * g + j) * N + n0 + 16 * ct + r16] = v[ii][ct][j];
-    return;
-  }
-  // FWHT-128 over the group's columns, stages lg = 0..6 in order (the lower index keeps a + b, the upper
-  // takes a - b): bits 0-3 are lane bits 0-3, bits 4-6 the column tile ct
-  unsigned short* C = (unsigned short*)p.c;
-#pragma unroll
-  for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float x[8];
-#pragma unroll
-      for (int ct = 0; ct < 8; ++ct) x[ct] = v[ii][ct][j];
-#pragma unroll
-      for (int mask = 1; mask <= 8; mask <<= 1) {
-        const bool upper = (lane & mask) != 0;
-#pragma unroll
-        for (int ct = 0; ct < 8; ++ct) {
-          const float o = __shfl_xor(x[ct], mask, 64);
-          x[ct] = upper ? o - x[ct] : x[ct] + o;
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (SC == kSCoarse) v[ii][ct][j] = (float)iacc[ii][ct][j] * (sav[j] * swc[ct]);
+          else if constexpr (SC == kSABlk) v[ii][ct][j] = facc[ii][ct][j] * swc[ct];
+          else v[ii][ct][j] = facc[ii][ct][j];
         }
-      }
-#pragma unroll
-      for (int b = 1; b <= 4; b <<= 1)
-#pragma unroll
-        for (int ct = 0; ct < 8; ++ct)
-          if ((ct & b) == 0) {
-            const float a0 = x[ct], b0 = x[ct | b];
-            x[ct] = a0 + b0;
-            x[ct | b] = a0 - b0;
-          }
-      const int r = 32 * wave + 16 * ii + 4 * g + j;
-#pragma unroll
-      for (int ct = 0; ct < 8; ++ct) {
-        const int n = n0 + 16 * ct + r16;
-        C[(size_t)r * N + n] = r4_bf16_rn((x[ct] * p.svh[n]) * p.out_scale);
-      }
     }
+    if (p.SKG > 1) {
+      float* dst = p.ws + (size_t)ky * 256 * N;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct) dst[(size_t)(32 * wave + 16 * ii + 4 * g + j) * N + n0 + 16 * ct + r16] = v[ii][ct][j];
+      return;
+    }
+    if constexpr (OUT == kOutF16) {
+      unsigned short* C = (unsigned short*)p.c;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct)
+            C[(size_t)(32 * wave + 16 * ii + 4 * g + j) * N + n0 + 16 * ct + r16] =
+                __builtin_bit_cast(unsigned short, (_Float16)v[ii][ct][j]);
+      return;
+    } else {
+      // FWHT-128 over the group's columns, stages lg = 0..6 in order (the lower index keeps a + b, the upper
+      // takes a - b): bits 0-3 are lane bits 0-3, bits 4-6 the column tile ct
+      unsigned short* C = (unsigned short*)p.c;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float x[8];
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct) x[ct] = v[ii][ct][j];
+#pragma unroll
+          for (int mask = 1; mask <= 8; mask <<= 1) {
+            const bool upper = (lane & mask) != 0;
+#pragma unroll
+            for (int ct = 0; ct < 8; ++ct) {
+              const float o = __shfl_xor(x[ct], mask, 64);
+              x[ct] = upper ? o - x[ct] : x[ct] + o;
+            }
+          }
+#pragma unroll
+          for (int b = 1; b <= 4; b <<= 1)
+#pragma unroll
+            for (int ct = 0; ct < 8; ++ct)
+              if ((ct & b) == 0) {
+                const float a0 = x[ct], b0 = x[ct | b];
+                x[ct] = a0 + b0;
+                x[ct | b] = a0 - b0;
+              }
+          const int r = 32 * wave + 16 * ii + 4 * g + j;
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct) {
+            const int n = n0 + 16 * ct + r16;
+            C[(size_t)r * N + n] = r4_bf16_rn((x[ct] * p.svh[n]) * p.out_scale);
+          }
+        }
+    }
+  }
+}
+
+// The second pass of a split dense launch: the SKG slices of ws added in slice order (as integers for the
+// int32 test entry), then stored as f16 (or int32).
+template <int OUT>
+__global__ __launch_bounds__(256) void ti8_finish_kernel(const void* __restrict__ ws, void* __restrict__ c, int M,
+                                                         int N, int SKG) {
+  const long long id = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (id >= (long long)M * N) return;
+  const size_t sy = (size_t)M * N;
+  if constexpr (OUT == kOutI32) {
+    int acc = 0;
+    for (int y = 0; y < SKG; ++y) acc += ((const int*)ws)[y * sy + id];
+    ((int*)c)[id] = acc;
+  } else {
+    float acc = ((const float*)ws)[id];
+    for (int y = 1; y < SKG; ++y) acc += ((const float*)ws)[y * sy + id];
+    ((unsigned short*)c)[id] = __builtin_bit_cast(unsigned short, (_Float16)acc);
+  }
 }
 
 std::string ti8_check(int M, int K, int N, int n_split, int KB, int skw, int skg) {
@@ -397,9 +474,9 @@ std::string ti8_check(int M, int K, int N, int n_split, int KB, int skw, int skg
   return "";
 }
 
-template <int KB, bool P128>
+template <int KB, int SC, int OUT, bool DENSE>
 void ti8_launch(const TI8Args& a, int N, int SKG, hipStream_t st) {
-  hipLaunchKernelGGL((ti8_gemm_kernel<KB, P128>), dim3(N / 128, SKG), dim3(512), 0, st, a);
+  hipLaunchKernelGGL((ti8_gemm_kernel<KB, SC, OUT, DENSE>), dim3(N / 128, SKG), dim3(512), 0, st, a);
 }
 
 void ti8_run(bool p128, int64_t a8_0, int64_t sa_0, int64_t a8_1, int64_t sa_1, int n_split, int64_t w, int64_t sw,
@@ -417,7 +494,7 @@ void ti8_run(bool p128, int64_t a8_0, int64_t sa_0, int64_t a8_1, int64_t sa_1, 
   a.sa[0] = (const float*)sa_0;
   a.sa[1] = a8_1 ? (const float*)sa_1 : (const float*)sa_0;
   a.n_split = n_split;
-  a.w = (const unsigned*)w;
+  a.w = (const void*)w;
   a.sw = (const float*)sw;
   a.svh = (const float*)svh;
   a.c = (void*)c;
@@ -428,9 +505,11 @@ void ti8_run(bool p128, int64_t a8_0, int64_t sa_0, int64_t a8_1, int64_t sa_1, 
   a.out_scale = out_scale;
   hipStream_t st = (hipStream_t)stream;
   if (KB == 4) {
-    if (p128) ti8_launch<4, true>(a, N, skg, st); else ti8_launch<4, false>(a, N, skg, st);
+    if (p128) ti8_launch<4, kSBlk, kOutBf16, false>(a, N, skg, st);
+    else ti8_launch<4, kSCoarse, kOutBf16, false>(a, N, skg, st);
   } else {
-    if (p128) ti8_launch<5, true>(a, N, skg, st); else ti8_launch<5, false>(a, N, skg, st);
+    if (p128) ti8_launch<5, kSBlk, kOutBf16, false>(a, N, skg, st);
+    else ti8_launch<5, kSCoarse, kOutBf16, false>(a, N, skg, st);
   }
   if (skg > 1) r4d::launch_split_finish(a.ws, a.svh, a.c, M, N, skg, 1, out_scale, st);
   r4d::launch_ok(entry);
@@ -475,9 +554,84 @@ void ti8_dump(bool col, int64_t w, int64_t sw, int64_t w8, int64_t wp, int K, in
   r4d::launch_ok(entry);
 }
 
+// ---- the dense int8 GEMM (W8 block layout weights) --------------------------------------------------------
+std::string dense_check(int M, int K, int N, int SKG) {
+  if (M != 256) return "M must be 256 (the prefill chunk)";
+  if (K <= 0 || N <= 0 || K % 128 || N % 128) return "K and N must be positive multiples of 128";
+  if ((long long)N * K >= (1LL << 32)) return "N K must be below 2^32 bytes";
+  if (SKG < 1 || SKG > 64 || (K / 128) % SKG) return "SKG must be 1..64 and divide K / 128";
+  return "";
+}
+
+void dense_run(int64_t a8, int64_t sa, int64_t w8, int64_t sw, int64_t c, int64_t ws, int M, int K, int N, int SKG,
+               int scale_mode, bool raw_i32, int64_t stream, const char* entry) {
+  r4d::require(entry, dense_check(M, K, N, SKG));
+  if (scale_mode < 0 || scale_mode > 2) r4d::fail(entry, "scale_mode must be 0 (row / column), 1 (per-128 "
+                                                         "activation, column weight) or 2 (per-128 both)");
+  if (!a8 || !w8 || !c || (!raw_i32 && (!sa || !sw))) r4d::fail(entry, "null buffer");
+  if (SKG > 1 && !ws) r4d::fail(entry, "a split launch (SKG > 1) needs ws");
+  TI8Args a{};
+  a.a8[0] = (const signed char*)a8;
+  a.sa[0] = a.sa[1] = (const float*)sa;
+  a.n_split = N;
+  a.w = (const void*)w8;
+  a.sw = (const float*)sw;
+  a.c = (void*)c;
+  a.ws = (float*)ws;
+  a.K = K;
+  a.N = N;
+  a.SKG = SKG;
+  a.out_scale = 1.f;
+  hipStream_t st = (hipStream_t)stream;
+  if (raw_i32) ti8_launch<4, kSCoarse, kOutI32, true>(a, N, SKG, st);
+  else if (scale_mode == 0) ti8_launch<4, kSCoarse, kOutF16, true>(a, N, SKG, st);
+  else if (scale_mode == 1) ti8_launch<4, kSABlk, kOutF16, true>(a, N, SKG, st);
+  else ti8_launch<4, kSBlk, kOutF16, true>(a, N, SKG, st);
+  if (SKG > 1) {
+    const long long n = (long long)M * N;
+    if (raw_i32)
+      hipLaunchKernelGGL(ti8_finish_kernel<kOutI32>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                         (const void*)ws, (void*)c, M, N, SKG);
+    else
+      hipLaunchKernelGGL(ti8_finish_kernel<kOutF16>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                         (const void*)ws, (void*)c, M, N, SKG);
+  }
+  r4d::launch_ok(entry);
+}
+
 }  // namespace
 
 extern "C" {
+
+const char* r4d_gemm_i8_dense_check(int M, int K, int N, int SKG) { return r4d::check_result(dense_check(M, K, N, SKG)); }
+size_t r4d_gemm_i8_dense_ws_bytes(int M, int N, int SKG) { return SKG > 1 ? (size_t)SKG * M * N * 4 : 0; }
+// The dense int8 GEMM: a8 in the A8 layout (r4d_trellis_i8_quant_act / _row), w8 in the W8 block layout
+// (r4d_i8_pack_w), C f16 [256][N]. scale_mode 0: sa [256], sw [N]; 1: sa [K/128][256], sw [N]; 2: sa
+// [K/128][256], sw [K/128][N]. SKG > 1: ws (ws_bytes); tickets accepted and unused.
+void r4d_gemm_i8_dense(int64_t a8, int64_t sa, int64_t w8, int64_t sw, int64_t c, int64_t ws, int64_t tickets, int M,
+                       int K, int N, int SKG, int scale_mode, int64_t stream) {
+  (void)tickets;
+  dense_run(a8, sa, w8, sw, c, ws, M, K, N, SKG, scale_mode, false, stream, "gemm_i8_dense");
+}
+// Test entry: the exact int32 sums C[m][n] = sum_k A[m][k] W[n][k] (int32 [256][N]) through the same kernel and
+// split.
+void r4d_gemm_i8_dense_raw(int64_t a8, int64_t w8, int64_t c, int64_t ws, int64_t tickets, int M, int K, int N,
+                           int SKG, int64_t stream) {
+  (void)tickets;
+  dense_run(a8, 0, w8, 0, c, ws, M, K, N, SKG, 0, true, stream, "gemm_i8_dense_raw");
+}
+// This build's K split for the dense int8 GEMM: the fewest slices (of at least 1024 k) that reach 128
+// workgroups -- the split that measured fastest at both config-4 shapes (1 at 5120 x 17408, 4 at 17408 x 5120).
+int r4d_mi355x_i8_skg(int K, int N) {
+  const int G = N / 128, nkb = K / 128;
+  int best = 1;
+  for (int d = 1; d <= 16; ++d) {
+    if (nkb % d || nkb / d < 8) continue;
+    best = d;
+    if ((long long)G * d >= 128) break;
+  }
+  return best;
+}
 
 // r4d.h:490 (K / 128) N floats
 size_t r4d_trellis_i8_wscale_count(int K, int N) { return (size_t)(K / 128) * (size_t)N; }
