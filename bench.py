@@ -71,6 +71,8 @@ def main():
         x = torch.from_numpy(WL.activations_f16(M, K, 30 + i)).to(dev)
         a = torch.empty((M, K), dtype=torch.float16, device=dev)
         skg = api.trellis_gemv_skg(K, N, KB)
+        while (K // 128) % skg:     # whole 128-blocks per slice (the fused transform's rule)
+            skg -= 1
         ws = torch.empty(max(1, skg * M * N), dtype=torch.float32, device=dev)
         tickets = api.TicketBuffer(N, dev).t
         out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
@@ -78,10 +80,16 @@ def main():
                         tickets=tickets, out=out))
     out_scale = float(np.float32(1.0 / np.sqrt(128.0)))
 
-    # Launches go to the current stream (the capture stream while a graph is being captured).
+    # Launches go to the current stream (the capture stream while a graph is being captured). The step is
+    # the engine's two launches per projection (input transform, then the GEMV on A); the fused entry
+    # (r4dx_trellis_gemv_xf: each workgroup transforms its own slice of x) is timed beside it.
     def gemv(L, copy):
         api.trellis_gemm_m64(L["a"], L["words"][copy], L["svh"], L["K"], L["N"], KB, skg=L["skg"],
                              out=L["out"], ws=L["ws"], tickets=L["tickets"], out_scale=out_scale)
+
+    def gemv_xf(L, copy):
+        api.trellis_gemv_xf(L["x"], L["suh"], L["words"][copy], L["svh"], L["K"], L["N"], KB, skg=L["skg"],
+                            out=L["out"], ws=L["ws"], tickets=L["tickets"], out_scale=out_scale)
 
     def step(c, gemv_only=False):
         for L in lin:
@@ -89,9 +97,14 @@ def main():
                 api.trellis_input(L["x"], [L["suh"]], 0, bf16=False, outs=[L["a"]])
             gemv(L, c)
 
+    def step_unfused(c):      # (the fused form)
+        for L in lin:
+            gemv_xf(L, c)
+
     # One HIP graph per sweep over the weight copies: a step per copy (Python launch cost out of the
     # timed region; the kernels are what a C++ caller would launch back to back).
     for c in range(copies):   # eager once: A is valid, tickets settle
+        step_unfused(c)
         step(c)
     torch.cuda.synchronize()
     if args.pmc:
@@ -136,6 +149,14 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = e0.elapsed_time(e1) / steps
+    g_unf = capture(lambda: [step_unfused(c) for c in range(copies)])
+    g_unf.replay()
+    u0, u1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    u0.record(stream)
+    g_unf.replay()
+    u1.record(stream)
+    torch.cuda.synchronize()
+    ms_step_unfused = u0.elapsed_time(u1) / copies
 
     # The dominant kernel alone: per shape, a graph of back-to-back launches over the rotating copies.
     R = 4
@@ -183,7 +204,9 @@ def main():
         "config": {"workload": f"config1: 10 projections of one 27B-class layer, M={M}, KB={KB}, "
                                f"{copies} rotating weight copies ({copies * layer_wbytes / 2**30:.2f} GiB)",
                    "M": M, "KB": KB, "weight_bytes_per_step": layer_wbytes,
-                   "step": "input transform + trellis GEMV (FWHT/svh epilogue, bf16 out) per projection"},
+                   "step": "per projection: input transform + trellis GEMV (FWHT/svh epilogue, bf16 out)",
+                   "fused_xf_ms_per_step": round(ms_step_unfused, 4),
+                   "fused_xf_GBs": round(layer_wbytes / (ms_step_unfused * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic("tq_gemv_kernel", KB, M),
                      "kernel": "tq_gemv_kernel", "avg_launch_us": round(gemv_ms * 1e3 / len(lin), 3),

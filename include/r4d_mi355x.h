@@ -45,6 +45,14 @@ const char* r4d_gemm_trellis_nt_m64_check(int M, int K, int N, int n_split, int 
 /* No reference counterpart (the reference reads gemm_tuning_table_trellis.inc): this build's SKG for
  * a shape, the same for every M. */
 int    r4d_mi355x_trellis_gemv_skg(int K, int N, int KB);
+/* No reference counterpart (the engine runs r4dx_trellis_input_bf16 then r4d_gemm_trellis_nt_m64): the two
+ * fused -- x f16 (x_is_bf16 = 0) or bf16 [M][K], suh0 (columns < n_split) / suh1 fp32 [K], prescale_log2 as the
+ * transform's -- each workgroup transforms its own K slice into LDS. Bit-identical to the two-launch path.
+ * Needs (K / 128) % SKG == 0 and the slice in LDS (r4dx_trellis_gemv_xf_check). */
+void r4dx_trellis_gemv_xf(int64_t x, int x_is_bf16, int64_t suh0, int64_t suh1, int n_split, int prescale_log2,
+                          int64_t w, int64_t svh, int64_t c, int64_t ws, int64_t tickets, int M, int K, int N, int KB,
+                          int SKG, float out_scale, int64_t stream);
+const char* r4dx_trellis_gemv_xf_check(int M, int K, int N, int n_split, int KB, int SKG, int have_ws);
 
 /* ---- trellis prefill GEMM, M = 128 or 256 ------------------------------------------------------ */
 /* r4d.h:416-419 r4d_gemm_trellis_nt_m256: the linear of r4d_gemm_trellis_nt_m64 for 128 or 256 rows

@@ -243,3 +243,29 @@ def trellis_gemm_i8(a8, sa, w, sw, svh, K, N, KB, coarse=False, a8_1=None, sa_1=
     f(_p(a8), _p(sa), _p(a8_1) if a8_1 is not None else 0, _p(sa_1) if sa_1 is not None else 0, n_split, _p(w), _p(sw),
       _p(svh), _p(out), _p(ws) if ws is not None else 0, 0, M, K, N, KB, skw, skg, out_scale, _stream(stream))
     return out
+
+
+def trellis_gemv_xf(x, suh, w, svh, K, N, KB, skg=None, suh1=None, n_split=None, prescale=0, bf16=False, out=None,
+                    ws=None, tickets=None, out_scale=1.0, stream=None):
+    """The input transform fused into the GEMV (r4dx_trellis_gemv_xf): x f16/bf16 bits [M][K] -> C bf16 [M][N]."""
+    L = lib()
+    M = x.shape[0]
+    if skg is None:   # the planner's split, lowered to whole 128-blocks per slice
+        skg = trellis_gemv_skg(K, N, KB)
+        while (K // 128) % skg:
+            skg -= 1
+    n_split = N if n_split is None else n_split
+    have_ws = skg > 1 or (ws is not None and tickets is not None)
+    msg = L.r4dx_trellis_gemv_xf_check(M, K, N, n_split, KB, skg, int(have_ws))
+    if msg:
+        raise ValueError(msg.decode())
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    if have_ws and ws is None:
+        ws = torch.empty(max(1, skg * M * N), dtype=torch.float32, device=x.device)
+    if have_ws and tickets is None:
+        tickets = TicketBuffer(N, x.device).t
+    L.r4dx_trellis_gemv_xf(_p(x), int(bf16), _p(suh), _p(suh1), n_split, prescale, _p(w), _p(svh), _p(out),
+                           _p(ws) if have_ws else 0, _p(tickets) if have_ws else 0, M, K, N, KB, skg, out_scale,
+                           _stream(stream))
+    return out

@@ -53,4 +53,8 @@ struct r4d_gemv_args {
   int M, K, N, KB, SKG, full;
   float out_scale;
   int64_t stream;
+  // the fused input transform (r4dx_trellis_gemv_xf): xf = 1 for f16 x, 2 for bf16 x in a0; suh per part
+  int64_t suh0, suh1;
+  int xf;
+  float xscale;
 };

@@ -86,12 +86,15 @@ __device__ __forceinline__ void load_words_ptr(Words<KB>& s, const unsigned* __r
 constexpr int kRedParts = 8;         // the final slice sum is 8 interleaved runs, added in order
 constexpr int kRedRows = 4;          // rows of the final slice sum per pass
 
-template <int KB, int MT, int NPW, bool ALDS>
+// XF > 0: A0 is the raw input x [M][K] (XF 1: f16, 2: bf16) and the workgroup stages its own slice of the
+// transformed A = f16(FWHT128(fp32(x) * suh) * xscale) (suh0 / suh1 by column part) straight into LDS --
+// the arithmetic of r4dx_trellis_input_*, so A is bit-identical to the unfused path's.
+template <int KB, int MT, int NPW, bool ALDS, int XF>
 __global__ __launch_bounds__(256) void tq_gemv_kernel(
     const unsigned short* __restrict__ A0, const unsigned short* __restrict__ A1, int n_split,
     const unsigned* __restrict__ W, const float* __restrict__ svh, void* __restrict__ Cv,
     float* __restrict__ ws, unsigned* __restrict__ tickets, int M, int K, int N, int SKG, int full,
-    float out_scale) {
+    float out_scale, const float* __restrict__ suh0, const float* __restrict__ suh1, float xscale) {
   constexpr int PF = 4;
   constexpr int NT = 256;
   constexpr int SK = 4 / NPW;
@@ -187,13 +190,75 @@ __global__ __launch_bounds__(256) void tq_gemv_kernel(
     }
   };
 
+  // Fused transform: the x and suh values of this wave's first (up to kXfPre) blocks are requested before
+  // the weight stream, so (loads completing in order) the transform does not wait behind the weights.
+  constexpr int kXfPre = 2;
+  float xpre[XF > 0 ? kXfPre : 1][4];
+  const int xf_nblk = (ktl_pad + 7) >> 3;
+  const float* __restrict__ suh_p = group * 128 >= n_split ? suh1 : suh0;
+  if constexpr (XF > 0) {
+#pragma unroll
+    for (int j = 0; j < kXfPre; ++j) {
+      const int u = wave + 4 * j, b = u / M, r = u - b * M;
+      xpre[j][0] = xpre[j][1] = xpre[j][2] = xpre[j][3] = 0.f;
+      if (u < xf_nblk * M && 8 * b < ktw) {
+        const size_t kb = (size_t)16 * kt0 + 128 * (size_t)b;
+        const unsigned short* xr = A0 + (size_t)r * K + kb;
+        xpre[j][0] = XF == 2 ? r4_bf16_to_f32(xr[lane]) : r4_f16_to_f32(xr[lane]);
+        xpre[j][1] = XF == 2 ? r4_bf16_to_f32(xr[lane + 64]) : r4_f16_to_f32(xr[lane + 64]);
+        xpre[j][2] = suh_p[kb + lane];
+        xpre[j][3] = suh_p[kb + 64 + lane];
+      }
+    }
+  }
   // The weight stream starts before A is staged, so its latency overlaps the staging.
   St ring[PF];
   if (nst > 0) {
 #pragma unroll
     for (int i = 0; i < PF; ++i) load(ring[i], i);
   }
-  if constexpr (ALDS) {
+  if constexpr (ALDS && XF > 0) {
+    // one wave per (128-block, row) of the slice: lane l transforms k = 128 b + l and + 64, and writes
+    // each f16 to its fragment slot -- element k16 of k-tile ktl sits at half (k16 >> 3) + 2 ((k16 >> 2)
+    // & 1) of the 32-byte (ktl, row) chunk (h = 0: k 0-3, 8-11; h = 1: k 4-7, 12-15); then the zero block.
+    unsigned short* ah = (unsigned short*)alds;
+    const int nblk = xf_nblk;
+#pragma unroll 1
+    for (int u = wave, j = 0; u < nblk * M; u += NT / 64, ++j) {
+      const int b = u / M, r = u - b * M;
+      unsigned short hv[2] = {0, 0};
+      if (8 * b < ktw) {
+        float x0, x1, s0, s1;
+        if (j < kXfPre) {
+          // (a constant index per unrolled copy is not needed: the preload array is tiny)
+          x0 = xpre[0][0]; x1 = xpre[0][1]; s0 = xpre[0][2]; s1 = xpre[0][3];
+#pragma unroll
+          for (int jj = 1; jj < kXfPre; ++jj)
+            if (j == jj) { x0 = xpre[jj][0]; x1 = xpre[jj][1]; s0 = xpre[jj][2]; s1 = xpre[jj][3]; }
+        } else {
+          const size_t kb = (size_t)16 * kt0 + 128 * (size_t)b;
+          const unsigned short* xr = A0 + (size_t)r * K + kb;
+          x0 = XF == 2 ? r4_bf16_to_f32(xr[lane]) : r4_f16_to_f32(xr[lane]);
+          x1 = XF == 2 ? r4_bf16_to_f32(xr[lane + 64]) : r4_f16_to_f32(xr[lane + 64]);
+          s0 = suh_p[kb + lane];
+          s1 = suh_p[kb + 64 + lane];
+        }
+        float v0 = x0 * s0;
+        float v1 = x1 * s1;
+        r4_fwht128_wave(v0, v1, lane);
+        hv[0] = r4_f16_rn(v0 * xscale);
+        hv[1] = r4_f16_rn(v1 * xscale);
+      }
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int kl = 128 * b + lane + 64 * e, ktl = kl >> 4, k16 = kl & 15;
+        if (ktl < ktl_pad)
+          ah[(size_t)(ktl * M + r) * 16 + (((k16 >> 3) & 1) + 2 * ((k16 >> 2) & 1)) * 4 + (k16 & 3)] = hv[e];
+      }
+    }
+    if (threadIdx.x < 16) ah[(size_t)ktl_pad * M * 16 + threadIdx.x] = 0;
+    __syncthreads();
+  } else if constexpr (ALDS) {
     // chunk (ktl, row, j): k 16 (kt0 + ktl) + 8j .. + 8 of A[row] -> halves of fragments h = 0, 1;
     // k-tiles past the slice are zero, and so is the 32-byte block after the copy (rows >= M read it).
     const int chunks = ktl_pad * M * 2;
@@ -383,23 +448,40 @@ size_t gemv_lds(int MT, int NPW, bool alds, int ktw, int M) {
 }
 constexpr size_t kAldsMax = 48 * 1024;   // A slices up to this many bytes are staged in LDS
 
-template <int KB, int MT, int NPW, bool ALDS>
+constexpr size_t kXfAldsMax = 96 * 1024;   // the fused transform stages the slice in LDS up to this size
+
+template <int KB, int MT, int NPW, bool ALDS, int XF>
 void launch_gemv(const r4d_gemv_args& a) {
   dim3 grid(a.N / 32 / NPW, a.SKG), block(256);
   const int ktw = a.K / 16 / a.SKG;
   const size_t smem = gemv_lds(MT, NPW, ALDS, ktw, a.M);
   if (smem > 160 * 1024) r4d::fail("gemm_trellis_nt_m64", "LDS request above 160 KiB");
-  hipLaunchKernelGGL((tq_gemv_kernel<KB, MT, NPW, ALDS>), grid, block, smem, (hipStream_t)a.stream,
+  static bool attr = false;
+  if (!attr && smem > 64 * 1024) {
+    (void)hipFuncSetAttribute((const void*)tq_gemv_kernel<KB, MT, NPW, ALDS, XF>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    attr = true;
+  }
+  hipLaunchKernelGGL((tq_gemv_kernel<KB, MT, NPW, ALDS, XF>), grid, block, smem, (hipStream_t)a.stream,
                      (const unsigned short*)a.a0, (const unsigned short*)(a.a1 ? a.a1 : a.a0), a.n_split,
                      (const unsigned*)a.w, (const float*)a.svh, (void*)a.c, (float*)a.ws,
-                     (unsigned*)a.tickets, a.M, a.K, a.N, a.SKG, a.full, a.out_scale);
+                     (unsigned*)a.tickets, a.M, a.K, a.N, a.SKG, a.full, a.out_scale, (const float*)a.suh0,
+                     (const float*)(a.suh1 ? a.suh1 : a.suh0), a.xscale);
 }
 
 template <int KB, int MT, int NPW>
 void launch_gemv_a(const r4d_gemv_args& a) {
   const int ktw = a.K / 16 / a.SKG;
-  if (gemv_ktl_pad(4 / NPW, ktw) * a.M * 32 <= kAldsMax) launch_gemv<KB, MT, NPW, true>(a);
-  else launch_gemv<KB, MT, NPW, false>(a);
+  const size_t abytes = gemv_ktl_pad(4 / NPW, ktw) * a.M * 32;
+  if (a.xf) {
+    if (abytes > kXfAldsMax) r4d::fail("trellis_gemv_xf", "the A slice does not fit LDS: raise SKG");
+    if (a.xf == 2) launch_gemv<KB, MT, NPW, true, 2>(a);
+    else launch_gemv<KB, MT, NPW, true, 1>(a);
+  } else if (abytes <= kAldsMax) {
+    launch_gemv<KB, MT, NPW, true, 0>(a);
+  } else {
+    launch_gemv<KB, MT, NPW, false, 0>(a);
+  }
 }
 
 // The split form (one pair per workgroup) whenever ws is there; the whole-group form for an
@@ -462,6 +544,39 @@ void r4d_gemm_trellis_nt_m64_raw(int64_t a0, int64_t a1, int n_split, int64_t w,
   (void)WV; (void)SK; (void)MT; (void)NP; (void)U; (void)NT; (void)clk;
   r4d_gemv_args a{a0, a1, n_split, w, 0, c, ws, tickets, M, K, N, KB, SKG, 0, 1.f, stream};
   tq_run(a, "gemm_trellis_nt_m64_raw");
+}
+
+// No reference counterpart: the input transform of r4dx_trellis_input_f16 / _bf16 fused into the GEMV.
+const char* r4dx_trellis_gemv_xf_check(int M, int K, int N, int n_split, int KB, int SKG, int have_ws) {
+  if (const char* m = r4d_gemm_trellis_nt_m64_check(M, K, N, n_split, KB, SKG, 1, 1, have_ws)) return m;
+  std::string e;
+  if ((K / 128) % SKG) e = "the fused transform needs whole 128-blocks per slice: (K / 128) % SKG == 0";
+  else {
+    const int NPW = (SKG == 1 && !have_ws) ? 4 : 1;
+    if (gemv_ktl_pad(4 / NPW, K / 16 / SKG) * M * 32 > kXfAldsMax) e = "the A slice does not fit LDS: raise SKG";
+  }
+  return r4d::check_result(e);
+}
+
+void r4dx_trellis_gemv_xf(int64_t x, int x_is_bf16, int64_t suh0, int64_t suh1, int n_split, int prescale_log2,
+                          int64_t w, int64_t svh, int64_t c, int64_t ws, int64_t tickets, int M, int K, int N, int KB,
+                          int SKG, float out_scale, int64_t stream) {
+  const char* entry = "trellis_gemv_xf";
+  if (!x || !suh0 || !w || !c) r4d::fail(entry, "null x, suh, W or C");
+  if (!suh1 && n_split != N) r4d::fail(entry, "a one-part launch (suh1 = 0) needs n_split = N");
+  if (prescale_log2 < -24 || prescale_log2 > 24) r4d::fail(entry, "|prescale_log2| must be <= 24");
+  if (const char* m = r4dx_trellis_gemv_xf_check(M, K, N, n_split, KB, SKG, ws != 0 && tickets != 0))
+    r4d::fail(entry, m);
+  r4d_gemv_args a{x, 0, n_split, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale, stream};
+  a.suh0 = suh0;
+  a.suh1 = suh1;
+  a.xf = x_is_bf16 ? 2 : 1;
+  // float(2^s / sqrt(128)), rounded once from double (trellis_ref.hpp:146-148)
+  a.xscale = (float)(__builtin_ldexp(1.0, prescale_log2) / __builtin_sqrt(128.0));
+  if (a.KB == 4) launch_gemv_kb<4>(a);
+  else if (a.KB == 5) launch_gemv_kb<5>(a);
+  else launch_gemv_kb<3>(a);
+  r4d::launch_ok(entry);
 }
 
 int r4d_gemm_trellis_nt_m64_has_rate(int KB) { return KB == 3 || KB == 4 || KB == 5; }

@@ -162,3 +162,28 @@ def test_config1_shapes_m1_m8(name, K, N):
             raw = api.trellis_gemm_m64(dev(a[:M]), w_d, None, K, N, KB, raw=True)
             torch.cuda.synchronize()
             assert close_rel(raw.cpu().numpy(), ref[:M], RAW_REL, RAW_FLOOR) <= 1.0, (KB, M)
+
+
+@pytest.mark.parametrize("KB,K,N,M,skg,bf16,prescale", [
+    (4, 5120, 17408, 1, None, False, 0), (4, 17408, 5120, 1, None, True, 3), (5, 5120, 1024, 8, None, False, -2),
+    (4, 6144, 5120, 4, 2, True, 0), (4, 1024, 512, 1, 1, False, 0), (3, 1024, 256, 2, 4, False, 1)])
+def test_gemv_fused_transform_bit_identical(KB, K, N, M, skg, bf16, prescale):
+    """r4dx_trellis_gemv_xf == r4dx_trellis_input_* + r4d_gemm_trellis_nt_m64, byte for byte (two parts)."""
+    banner("gemv xf", KB, K, N, M, skg, bf16, prescale)
+    rng = np.random.default_rng(K + N + M)
+    words = dev(WL.trellis_words(K, N, KB, 7))
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to("cuda")
+    xb = (x.to(torch.bfloat16) if bf16 else x.half()).view(torch.int16)
+    suh0, suh1 = dev(WL.signs(K, 8)), dev(WL.signs(K, 9))
+    svh = dev(WL.svh_scales(N, 10))
+    if skg is None:
+        skg = api.trellis_gemv_skg(K, N, KB)
+        while (K // 128) % skg:
+            skg -= 1
+    n_split = N // 2 if N >= 256 else N
+    a0, a1 = api.trellis_input(xb, [suh0, suh1], prescale, bf16=bf16)
+    ref = api.trellis_gemm_m64(a0, words, svh, K, N, KB, skg=skg, a1=a1, n_split=n_split, out_scale=0.0883883)
+    got = api.trellis_gemv_xf(xb, suh0, words, svh, K, N, KB, skg=skg, suh1=suh1, n_split=n_split,
+                              prescale=prescale, bf16=bf16, out_scale=0.0883883)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
