@@ -118,6 +118,15 @@ void r4d_trellis_i8_quant_act(int64_t x, int64_t a8, int64_t sa, int parts, int6
 /* r4d.h:517-518 r4d_trellis_i8_quant_act_row: the same with one scale per row, SA [256] per part. */
 void r4d_trellis_i8_quant_act_row(int64_t x, int64_t a8, int64_t sa, int parts, int64_t part_stride, int K,
                                   int64_t stream);
+/* kernels.h:149-161 r4dx_trellis_input_i8: r4dx_trellis_input_bf16's arguments and arithmetic up to the f16 A, which
+ * is not stored: each (row, 128-block) goes through r4d_trellis_i8_quant_act's quantizer into a8[o] (A8 layout)
+ * and sa[o] ([K/128][256]) -- byte for byte the two-step result. M must be 256. */
+void r4dx_trellis_input_i8(int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh, const int64_t* a8,
+                           const int64_t* sa, int prescale_log2, int64_t stream);
+/* kernels.h:167-175 r4dx_trellis_input_i8r: the same with one scale per row (sa[o] [256]), as
+ * r4d_trellis_i8_quant_act_row; the row's f16 values wait in LDS (nout K 2 bytes, at most 160 KiB). */
+void r4dx_trellis_input_i8r(int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh, const int64_t* a8,
+                            const int64_t* sa, int prescale_log2, int64_t stream);
 /* No reference counterpart: the same quantizers for any M into a plain row-major a8 [M][K] (for callers
  * that keep int8 activations row-major); blk != 0: sa [K/128][M], else sa [M]. */
 void r4d_i8_quant_act_plain(int64_t x, int64_t a8, int64_t sa, int M, int K, int blk, int64_t stream);

@@ -98,6 +98,137 @@ __global__ __launch_bounds__(256) void q_blk_kernel(const unsigned short* __rest
   if ((lane & 1) == 0) q_store4(a8 + (size_t)part * M * K, ref_layout, row, kb * 128 + 2 * lane, K, q01 | (q23 << 16));
 }
 
+// ---- the input transform fused with the quantizers (kernels.h:149-179) --------------------------------------
+// The transform's f16 A (r4dx_trellis_input_bf16's arithmetic: f16(FWHT128(fp32(x) * suh) * scale)) is not
+// stored; each (row, 128-block) goes through the quantizers above, byte for byte what r4d_trellis_i8_quant_act(_row)
+// makes from the stored A. x is bf16 [256][K]; output o gets suh[o], a8[o] (A8 layout) and sa[o].
+constexpr int kXqMaxOut = 3;
+struct XqOut {
+  const float* suh[kXqMaxOut];
+  signed char* a8[kXqMaxOut];
+  float* sa[kXqMaxOut];
+};
+// the transformed block of (row, k0) for output o: lane l gets the f16 bits of elements l and l + 64
+__device__ __forceinline__ void xq_transform(float x0, float x1, const float* __restrict__ suh, size_t k0, int lane,
+                                             float scale, unsigned short& h0, unsigned short& h1) {
+  float v0 = x0 * suh[k0 + lane];
+  float v1 = x1 * suh[k0 + 64 + lane];
+  r4_fwht128_wave(v0, v1, lane);
+  h0 = r4_f16_rn(v0 * scale);
+  h1 = r4_f16_rn(v1 * scale);
+}
+
+// per-(row, 128) scales: one wave per (row, block); the block goes through a wave-private LDS slot to reach
+// q_blk_kernel's lane map (lane l: k = 2 l, 2 l + 1)
+__global__ __launch_bounds__(256) void xq_blk_kernel(const unsigned short* __restrict__ x, int K, int nout, XqOut p,
+                                                     float scale) {
+  __shared__ unsigned short buf[4][128];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nkb = K >> 7;
+  const long long id = (long long)blockIdx.x * 4 + w;
+  if (id >= 256LL * nkb) return;
+  const int row = (int)(id / nkb), kb = (int)(id % nkb);
+  const size_t k0 = (size_t)kb * 128;
+  const unsigned short* xr = x + (size_t)row * K + k0;
+  const float x0 = r4_bf16_to_f32(xr[lane]), x1 = r4_bf16_to_f32(xr[lane + 64]);
+  for (int o = 0; o < nout; ++o) {
+    unsigned short h0, h1;
+    xq_transform(x0, x1, p.suh[o], k0, lane, scale, h0, h1);
+    buf[w][lane] = h0;
+    buf[w][lane + 64] = h1;
+    // the wave reads what other lanes wrote: keep the read after the writes (and the next output's writes
+    // after this read) -- without the clobber the compiler hoists the read above the stores
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const unsigned raw = *(const unsigned*)&buf[w][2 * lane];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const float v0 = r4_f16_to_f32((unsigned short)(raw & 0xFFFFu)), v1 = r4_f16_to_f32((unsigned short)(raw >> 16));
+    float amax = __builtin_fmaxf(__builtin_fabsf(v0), __builtin_fabsf(v1));
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, m, 64));
+    const float s = q_scale(amax);
+    if (lane == 0) p.sa[o][(size_t)kb * 256 + row] = s;
+    const unsigned q01 = ((unsigned)q_one(v0, s) & 0xFFu) | (((unsigned)q_one(v1, s) & 0xFFu) << 8);
+    const unsigned q23 = (unsigned)__shfl_xor((int)q01, 1, 64);
+    if ((lane & 1) == 0) q_store4(p.a8[o], true, row, (int)k0 + 2 * lane, K, q01 | (q23 << 16));
+  }
+}
+
+// one scale per row: a workgroup (4 waves) per row transforms every block into LDS (f16, [nout][K]), takes the
+// row's amax, then quantizes like q_row_kernel
+__global__ __launch_bounds__(256) void xq_row_kernel(const unsigned short* __restrict__ x, int K, int nout, XqOut p,
+                                                     float scale) {
+  extern __shared__ unsigned short rowbuf[];
+  __shared__ float red[kXqMaxOut][4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row = blockIdx.x, nkb = K >> 7;
+  float amax[kXqMaxOut] = {0.f, 0.f, 0.f};
+  for (int kb = w; kb < nkb; kb += 4) {
+    const size_t k0 = (size_t)kb * 128;
+    const unsigned short* xr = x + (size_t)row * K + k0;
+    const float x0 = r4_bf16_to_f32(xr[lane]), x1 = r4_bf16_to_f32(xr[lane + 64]);
+#pragma unroll
+    for (int o = 0; o < kXqMaxOut; ++o) {
+      if (o >= nout) break;
+      unsigned short h0, h1;
+      xq_transform(x0, x1, p.suh[o], k0, lane, scale, h0, h1);
+      rowbuf[(size_t)o * K + k0 + lane] = h0;
+      rowbuf[(size_t)o * K + k0 + lane + 64] = h1;
+      amax[o] = __builtin_fmaxf(amax[o], __builtin_fmaxf(__builtin_fabsf(r4_f16_to_f32(h0)), __builtin_fabsf(r4_f16_to_f32(h1))));
+    }
+  }
+#pragma unroll
+  for (int o = 0; o < kXqMaxOut; ++o) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) amax[o] = __builtin_fmaxf(amax[o], __shfl_xor(amax[o], m, 64));
+    if (lane == 0) red[o][w] = amax[o];
+  }
+  __syncthreads();
+  for (int o = 0; o < nout; ++o) {
+    const float s = q_scale(__builtin_fmaxf(__builtin_fmaxf(red[o][0], red[o][1]), __builtin_fmaxf(red[o][2], red[o][3])));
+    if (threadIdx.x == 0) p.sa[o][row] = s;
+    for (int k = threadIdx.x * 4; k < K; k += 1024) {
+      float v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = r4_f16_to_f32(rowbuf[(size_t)o * K + k + j]);
+      q_store4(p.a8[o], true, row, k, K, q_pack4(v, s));
+    }
+  }
+}
+
+void xq_run(bool row_scale, int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh, const int64_t* a8,
+            const int64_t* sa, int prescale_log2, int64_t stream, const char* entry) {
+  if (M != 256) r4d::fail(entry, "M must be 256 (the A8 layout's rows)");
+  if (K <= 0 || K % 128) r4d::fail(entry, "K must be a positive multiple of 128");
+  if (nout < 1 || nout > kXqMaxOut) r4d::fail(entry, "nout must be 1..3");
+  if (prescale_log2 < -24 || prescale_log2 > 24) r4d::fail(entry, "|prescale_log2| must be <= 24");
+  if (!x || !suh || !a8 || !sa) r4d::fail(entry, "null pointer");
+  XqOut p{};
+  for (int o = 0; o < nout; ++o) {
+    if (!suh[o] || !a8[o] || !sa[o]) r4d::fail(entry, "null suh, a8 or sa");
+    p.suh[o] = (const float*)suh[o];
+    p.a8[o] = (signed char*)a8[o];
+    p.sa[o] = (float*)sa[o];
+  }
+  // float(2^s / sqrt(128)), rounded once from double (trellis_ref.hpp:146-148)
+  const float scale = (float)(__builtin_ldexp(1.0, prescale_log2) / __builtin_sqrt(128.0));
+  hipStream_t st = (hipStream_t)stream;
+  if (row_scale) {
+    const size_t lds = (size_t)nout * K * 2;
+    // the row's values plus the kernel's 48 static bytes must fit the 160 KiB of a workgroup
+    if (lds > 160 * 1024 - 256) r4d::fail(entry, "nout K 2 bytes must stay below 160 KiB of LDS");
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute((const void*)xq_row_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess)
+      r4d::fail(entry, "hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
+    hipLaunchKernelGGL(xq_row_kernel, dim3(256), dim3(256), lds, st, (const unsigned short*)x, (int)K, nout, p, scale);
+  } else {
+    const long long waves = 256LL * (K / 128);
+    hipLaunchKernelGGL(xq_blk_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, (const unsigned short*)x,
+                       (int)K, nout, p, scale);
+  }
+  r4d::launch_ok(entry);
+}
+
 // plain int8 [N][K] -> the W8 block layout (r4d_trellis_i8_layout.h:24-27): one thread per output
 // dword, which is four consecutive k of one column
 __global__ __launch_bounds__(256) void w8_pack_kernel(const signed char* __restrict__ wp, unsigned* __restrict__ w8,
@@ -153,6 +284,16 @@ void r4d_i8_quant_act_plain(int64_t x, int64_t a8, int64_t sa, int M, int K, int
   quant_run(blk != 0, x, a8, sa, 1, 0, M, K, false, stream, "i8_quant_act_plain");
 }
 
+// kernels.h:160-161: the input transform fused with the per-(row, 128) quantizer
+void r4dx_trellis_input_i8(int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh, const int64_t* a8,
+                           const int64_t* sa, int prescale_log2, int64_t stream) {
+  xq_run(false, x, M, K, nout, suh, a8, sa, prescale_log2, stream, "trellis_input_i8");
+}
+// kernels.h:174-175: ... with one scale per row
+void r4dx_trellis_input_i8r(int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh, const int64_t* a8,
+                            const int64_t* sa, int prescale_log2, int64_t stream) {
+  xq_run(true, x, M, K, nout, suh, a8, sa, prescale_log2, stream, "trellis_input_i8r");
+}
 // plain int8 [N][K] -> W8 block layout (N K bytes), once per weight
 void r4d_i8_pack_w(int64_t wp, int64_t w8, int N, int K, int64_t stream) {
   if (N <= 0 || K <= 0 || N % 32 || K % 16) r4d::fail("i8_pack_w", "N must be a multiple of 32 and K of 16");

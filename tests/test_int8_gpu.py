@@ -142,3 +142,22 @@ def test_config4(K, N):
         c = api.i8_dense_gemm(a8, sa, w_d, dev(sw), K, N, scale_mode=mode)
         torch.cuda.synchronize()
         assert close_rel(c.float().cpu().numpy(), _oracle_mode(x, w8, sw, mode), 1e-3, 1e-4) <= 1.0
+
+
+@pytest.mark.parametrize("row_scale", [False, True])
+@pytest.mark.parametrize("K,nout,prescale", [(5120, 1, 0), (17408, 1, 3), (1024, 2, -4), (2048, 3, 0)])
+def test_fused_transform_quantizer_bit_exact(row_scale, K, nout, prescale):
+    """r4dx_trellis_input_i8(r) == r4dx_trellis_input_bf16 then r4d_trellis_i8_quant_act(_row), byte for byte."""
+    banner("xq", row_scale, K, nout, prescale)
+    rng = np.random.default_rng(K + nout)
+    x = torch.from_numpy(rng.standard_t(4, (256, K)).astype(np.float32)).to("cuda").to(torch.bfloat16).view(torch.int16)
+    suh = [dev(WL.signs(K, 40 + o)) for o in range(nout)]
+    got = api.trellis_input_i8(x, suh, prescale, row_scale)
+    outs = api.trellis_input(x, suh, prescale, bf16=True)
+    torch.cuda.synchronize()
+    for o in range(nout):
+        a8, sa = api.i8_quant(outs[o], blk=not row_scale, ref_layout=True)
+        torch.cuda.synchronize()
+        assert torch.equal(got[o][1].view(torch.int32), sa.view(torch.int32)), \
+            (o, int((got[o][1] != sa).sum()), got[o][1][:4].tolist(), sa[:4].tolist())
+        assert torch.equal(got[o][0], a8), (o, int((got[o][0] != a8).sum()))
