@@ -97,14 +97,14 @@ def main():
                 api.trellis_input(L["x"], [L["suh"]], 0, bf16=False, outs=[L["a"]])
             gemv(L, c)
 
-    def step_unfused(c):      # (the fused form)
+    def step_fused(c):
         for L in lin:
             gemv_xf(L, c)
 
     # One HIP graph per sweep over the weight copies: a step per copy (Python launch cost out of the
     # timed region; the kernels are what a C++ caller would launch back to back).
     for c in range(copies):   # eager once: A is valid, tickets settle
-        step_unfused(c)
+        step_fused(c)
         step(c)
     torch.cuda.synchronize()
     if args.pmc:
@@ -149,14 +149,14 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = e0.elapsed_time(e1) / steps
-    g_unf = capture(lambda: [step_unfused(c) for c in range(copies)])
-    g_unf.replay()
+    g_fused = capture(lambda: [step_fused(c) for c in range(copies)])
+    g_fused.replay()
     u0, u1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     u0.record(stream)
-    g_unf.replay()
+    g_fused.replay()
     u1.record(stream)
     torch.cuda.synchronize()
-    ms_step_unfused = u0.elapsed_time(u1) / copies
+    ms_step_fused = u0.elapsed_time(u1) / copies
 
     # The dominant kernel alone: per shape, a graph of back-to-back launches over the rotating copies.
     R = 4
@@ -205,8 +205,8 @@ def main():
                                f"{copies} rotating weight copies ({copies * layer_wbytes / 2**30:.2f} GiB)",
                    "M": M, "KB": KB, "weight_bytes_per_step": layer_wbytes,
                    "step": "per projection: input transform + trellis GEMV (FWHT/svh epilogue, bf16 out)",
-                   "fused_xf_ms_per_step": round(ms_step_unfused, 4),
-                   "fused_xf_GBs": round(layer_wbytes / (ms_step_unfused * 1e-3) / 1e9, 1)},
+                   "fused_xf_ms_per_step": round(ms_step_fused, 4),
+                   "fused_xf_GBs": round(layer_wbytes / (ms_step_fused * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic("tq_gemv_kernel", KB, M),
                      "kernel": "tq_gemv_kernel", "avg_launch_us": round(gemv_ms * 1e3 / len(lin), 3),
@@ -431,8 +431,13 @@ def bench_trellis_i8(api, WL, KB, R=4):
         out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
         skg = 1 if N > 8192 else 4
         ws = torch.empty(max(1, skg * M * N), dtype=torch.float32, device=dev)
+        xb = torch.from_numpy(WL.activations_f16(M, K, 7, outlier_frac=0.01).astype("float32")).to(dev) \
+            .to(torch.bfloat16).view(torch.int16)
+        suh = torch.from_numpy(WL.signs(K, 9)).to(dev)
         for coarse in (False, True):
             a8, sa = api.i8_quant(x, blk=not coarse, ref_layout=True)
+            # the fused input transform + quantizer that feeds this GEMM (bf16 x -> a8, sa)
+            in_ms = _graph_ms(lambda: api.trellis_input_i8(xb, [suh], 0, coarse, outs=[(a8, sa)]), 8, 1)
             sws = [api.trellis_i8_table(w, K, N, KB, coarse) for w in words]
 
             def gemm():
@@ -443,7 +448,8 @@ def bench_trellis_i8(api, WL, KB, R=4):
             ops = 2.0 * M * K * N
             res[f"K{K}_N{N}_{'coarse' if coarse else 'per128'}"] = {
                 "gemm_us": round(ms * 1e3, 2), "TOPs": round(ops / (ms * 1e-3) / 1e12, 1),
-                "frac_int8_peak": round(ops / (ms * 1e-3) / 5.0e15, 4), "skg": skg}
+                "frac_int8_peak": round(ops / (ms * 1e-3) / 5.0e15, 4), "skg": skg,
+                "input_i8_us": round(in_ms * 1e3, 2)}
         del words
         torch.cuda.empty_cache()
     return {"metric": "int8 x int8 trellis prefill GEMM TOP/s (M=256, KB4)", "kernel": "ti8_gemm_kernel",

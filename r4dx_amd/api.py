@@ -271,13 +271,17 @@ def trellis_gemv_xf(x, suh, w, svh, K, N, KB, skg=None, suh1=None, n_split=None,
     return out
 
 
-def trellis_input_i8(x, suh_list, prescale=0, row_scale=False, stream=None):
+def trellis_input_i8(x, suh_list, prescale=0, row_scale=False, outs=None, stream=None):
     """The input transform fused with the activation quantizer (r4dx_trellis_input_i8 / _i8r): x bf16 bits
-    [256][K] -> per output (a8 A8 layout, sa [K/128][256] or [256])."""
+    [256][K] -> per output (a8 A8 layout, sa [K/128][256] or [256]); outs: preallocated (a8, sa) pairs."""
     M, K = x.shape
     n = len(suh_list)
-    a8 = [torch.empty(M * K, dtype=torch.int8, device=x.device) for _ in range(n)]
-    sa = [torch.empty(M if row_scale else (K // 128) * M, dtype=torch.float32, device=x.device) for _ in range(n)]
+    if outs is None:
+        outs = [(torch.empty(M * K, dtype=torch.int8, device=x.device),
+                 torch.empty(M if row_scale else (K // 128) * M, dtype=torch.float32, device=x.device))
+                for _ in range(n)]
+    a8 = [o[0] for o in outs]
+    sa = [o[1] for o in outs]
     arr = lambda ts: (C.c_int64 * n)(*[t.data_ptr() for t in ts])
     f = lib().r4dx_trellis_input_i8r if row_scale else lib().r4dx_trellis_input_i8
     f(_p(x), M, K, n, arr(suh_list), arr(a8), arr(sa), prescale, _stream(stream))
