@@ -7,9 +7,12 @@
  * (as the reference's do); every GEMM family also has a _check entry that returns NULL or a message
  * (valid until the calling thread's next check) without launching.
  *
- * Tuning knobs of the reference signatures (WV, SK, MT, NP, U, NT, skw) are accepted and ignored:
+ * Tuning knobs of the reference signatures (WV, MT, NP, U, NT, skw) are accepted and ignored:
  * this build plans its own geometry.  SKG (the grid K split) is honoured, because the caller sizes
- * ws by it; results depend on (K, N, KB, SKG) and never on M.
+ * ws by it.  SK of the M <= 64 GEMM chooses the summation order: SK = 1 runs one wave per tile pair
+ * over the whole K slice (the order r4d_gemm_trellis_nt_m256 reproduces); any other SK, with ws and
+ * tickets given or SKG > 1, splits each slice over 4 waves added in k order (an unsplit launch without
+ * ws always runs the SK = 1 form).  Results depend on (K, N, KB, SKG, that form) and never on M.
  */
 #ifndef R4D_MI355X_H
 #define R4D_MI355X_H
@@ -58,7 +61,9 @@ const char* r4dx_trellis_gemv_xf_check(int M, int K, int N, int n_split, int KB,
 /* r4d.h:416-419 r4d_gemm_trellis_nt_m256: the linear of r4d_gemm_trellis_nt_m64 for 128 or 256 rows
  * (two launches when SKG > 1: the slices, then their sum and the epilogue); ws fp32 ws_bytes(M, N,
  * SKG) required when SKG > 1 (the reference always requires it); tickets accepted and unused;
- * (K/16) must be divisible by 4 SKG. SK, NP, U, skw accepted and unused. */
+ * (K/16) must be divisible by 4 SKG. Every element equals, bit for bit, r4d_gemm_trellis_nt_m64's at
+ * M = 64 with SK = 1 and the same SKG (r4d.h:402-412); SK must be 0 or 1 (0 means 1), since SK > 1 names
+ * the 4-wave split order, which this kernel does not reproduce (_check says so). NP, U, skw unused. */
 void r4d_gemm_trellis_nt_m256(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
                               int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SK, int NP,
                               int SKG, int U, float out_scale, int64_t stream, int skw);

@@ -57,4 +57,7 @@ struct r4d_gemv_args {
   int64_t suh0, suh1;
   int xf;
   float xscale;
+  // SK = 1: one wave per tile pair over the whole K slice (the workgroup holds a 128-column group) also
+  // when the launch is split -- the summation order r4d_gemm_trellis_nt_m256 reproduces
+  int sk1;
 };

@@ -484,11 +484,11 @@ void launch_gemv_a(const r4d_gemv_args& a) {
   }
 }
 
-// The split form (one pair per workgroup) whenever ws is there; the whole-group form for an
-// unsplit launch without ws.
+// The whole-group form (one wave per pair over the slice) at SK = 1 or for an unsplit launch without ws;
+// else the split form (one pair per workgroup, its slice split over 4 waves).
 template <int KB, int MT>
 void launch_gemv_np(const r4d_gemv_args& a) {
-  if (a.SKG == 1 && (a.ws == 0 || a.tickets == 0)) launch_gemv_a<KB, MT, 4>(a);
+  if (a.sk1 || (a.SKG == 1 && (a.ws == 0 || a.tickets == 0))) launch_gemv_a<KB, MT, 4>(a);
   else launch_gemv_a<KB, MT, 1>(a);
 }
 
@@ -533,16 +533,18 @@ static void tq_run(r4d_gemv_args& a, const char* entry) {
 void r4d_gemm_trellis_nt_m64(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
                              int64_t ws, int64_t tickets, int M, int K, int N, int KB, int WV, int SK,
                              int MT, int NP, int SKG, int U, int NT, float out_scale, int64_t stream) {
-  (void)WV; (void)SK; (void)MT; (void)NP; (void)U; (void)NT;
+  (void)WV; (void)MT; (void)NP; (void)U; (void)NT;
   r4d_gemv_args a{a0, a1, n_split, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale, stream};
+  a.sk1 = SK == 1;
   tq_run(a, "gemm_trellis_nt_m64");
 }
 
 void r4d_gemm_trellis_nt_m64_raw(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t c, int64_t ws,
                                  int64_t tickets, int M, int K, int N, int KB, int WV, int SK, int MT,
                                  int NP, int SKG, int U, int NT, int64_t clk, int64_t stream) {
-  (void)WV; (void)SK; (void)MT; (void)NP; (void)U; (void)NT; (void)clk;
+  (void)WV; (void)MT; (void)NP; (void)U; (void)NT; (void)clk;
   r4d_gemv_args a{a0, a1, n_split, w, 0, c, ws, tickets, M, K, N, KB, SKG, 0, 1.f, stream};
+  a.sk1 = SK == 1;
   tq_run(a, "gemm_trellis_nt_m64_raw");
 }
 

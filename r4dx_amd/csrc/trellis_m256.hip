@@ -32,13 +32,19 @@ __device__ __forceinline__ r4_rsrc mk_rsrc(const void* p, unsigned bytes) {
 //     128-byte row segment) and the words of tile pair p, decodes them, and writes both into the stage;
 //   * 4 math waves: math wave (rh, ch) owns rows [rh M/2, +M/2) x columns [64 ch, +64) of the group =
 //     RT = M / 32 row tiles x 4 column tiles of v_mfma_f32_16x16x32_f16, reading A and B from LDS.
-// A and B are both stored in natural k order (A [row][64 k], B [16-byte chunk of 8 k][column], f16):
-// the decode's fragments (element e of half h <-> k = 8 (e >> 2) + 4 h + (e & 3)) are re-paired
-// in registers into the natural 16-byte chunks k 0-7 and 8-15 of a k-tile before the store. The 16-byte
-// chunk c of row r sits at slot c ^ ((r >> 1) & 7), so the 16 rows a fragment read touches use 16 distinct
-// bank groups.
+// A and B are stored in the M <= 64 kernel's MFMA operand order, so that every output element sees the
+// same MFMAs with the same operands in the same order and the results agree bit for bit: the 16-byte
+// chunk 4 h + g of a step holds fragment half h of k-tile g (element e <-> k = 8 (e >> 2) + 4 h + (e & 3)),
+// and MFMA half kh reads chunks 4 kh + 0..3. A is [row][8 chunks], written as 8-byte quads (a lane's
+// natural 8 k split into its h = 0 and h = 1 quads); B is [chunk][column], the decode's d[cs][h] as is.
+// Chunk c of row r sits at slot c ^ m2_swz(r), so the 16 rows a fragment read touches use 16 distinct
+// bank groups. (Natural-order A chunks with 16-byte writes measured ~3 % faster, but pair k differently
+// inside an MFMA; reading them back as two 8-byte halves costs 25 % in read conflicts.)
 constexpr int kM2Waves = 8;
-__device__ __forceinline__ int m2_slot(int r, int c) { return (r * 8 + (c ^ ((r >> 1) & 7))) * 16; }
+// j = (r >> 1) & 7 with bit 2 flipped by bit 0: still 16 distinct slots for a fragment read's 16 rows, and
+// the 8-byte quad writes of 8 consecutive rows (4 chunks per row and half h) use both 64-byte chunk groups
+__device__ __forceinline__ int m2_swz(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int m2_slot(int r, int c) { return (r * 8 + (c ^ m2_swz(r))) * 16; }
 // B is [chunk][column] instead: a decode lane writes columns 32 p + 16 t + 8 cs + c, so column bit 3 is
 // flipped on odd 16-column tiles to keep the t = 0 and t = 1 lanes of one write on different banks; a
 // fragment read (16 consecutive columns of one chunk) stays a permutation of 16 bank slots.
@@ -97,15 +103,23 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
     };
     auto put = [&](const St& s, int st) {
       unsigned char* stg = lds + (st & 1) * kStage;
+      // chunk 4 h + g of a row = fragment half h of k-tile g (k 4h..4h+3, 8+4h..8+4h+3), the M <= 64
+      // kernel's MFMA operand order: the lane's 8 natural k (ac even: k 0-7, odd: 8-15 of k-tile ac >> 1)
+      // split into its h = 0 and h = 1 quads
 #pragma unroll
-      for (int u = 0; u < AU; ++u) *(r4u4*)(stg + m2_slot(ar0 + 8 * u, ac)) = s.a[u];
+      for (int u = 0; u < AU; ++u) {
+        unsigned char* row = stg + (ac & 1) * 8;
+        *(r4u2*)(row + m2_slot(ar0 + 8 * u, ac >> 1)) = (r4u2){s.a[u][0], s.a[u][1]};
+        *(r4u2*)(row + m2_slot(ar0 + 8 * u, 4 + (ac >> 1))) = (r4u2){s.a[u][2], s.a[u][3]};
+      }
       unsigned d[2][2][4];
       r4_decode<KB>(s.w, d);
 #pragma unroll
       for (int cs = 0; cs < 2; ++cs) {
         const int n = 32 * p + 16 * t + 8 * cs + c;
-        *(r4u4*)(stg + kA + m2_bslot(n, 2 * q)) = (r4u4){d[cs][0][0], d[cs][0][1], d[cs][1][0], d[cs][1][1]};
-        *(r4u4*)(stg + kA + m2_bslot(n, 2 * q + 1)) = (r4u4){d[cs][0][2], d[cs][0][3], d[cs][1][2], d[cs][1][3]};
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          *(r4u4*)(stg + kA + m2_bslot(n, 4 * h + q)) = (r4u4){d[cs][h][0], d[cs][h][1], d[cs][h][2], d[cs][h][3]};
       }
     };
     constexpr int PF = 2;
@@ -270,15 +284,23 @@ __global__ __launch_bounds__(256) void tq_m256_finish(const float* __restrict__ 
   const int col = threadIdx.x & 127, rh = threadIdx.x >> 7;
   const int n0 = group * 128;
   const size_t sy = (size_t)M * N;
+  // the M <= 64 kernel's slice order: run p (0..7) = 0.f + slices p, p + 8, ... in order, then the 8 runs
+  // added in order 0..7
   float v[16];
+#pragma unroll 1
+  for (int p = 0; p < 8; ++p) {
+    float run[16];
 #pragma unroll
-  for (int u = 0; u < 16; ++u) v[u] = ws[(size_t)(r0 + rh + 2 * u) * N + n0 + col];
-  for (int y = 1; y < SKG; ++y) {
-    float t[16];
+    for (int u = 0; u < 16; ++u) run[u] = 0.f;
+    for (int y = p; y < SKG; y += 8) {
+      float t[16];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) t[u] = ws[(size_t)y * sy + (size_t)(r0 + rh + 2 * u) * N + n0 + col];
+      for (int u = 0; u < 16; ++u) t[u] = ws[(size_t)y * sy + (size_t)(r0 + rh + 2 * u) * N + n0 + col];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) v[u] += t[u];
+      for (int u = 0; u < 16; ++u) run[u] += t[u];
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = p == 0 ? run[u] : v[u] + run[u];
   }
   if (!full) {
     float* Cf = (float*)Cv;
@@ -361,20 +383,27 @@ void r4d::launch_split_finish(const float* ws, const float* svh, void* c, int M,
   hipLaunchKernelGGL(tq_m256_finish, dim3(N / 128, M / 32), dim3(256), 0, st, ws, svh, c, M, N, SKG, full, out_scale);
 }
 
+static const char* const sk_msg =
+    "SK must be 1 (or 0): the M <= 64 row this reproduces is r4d_gemm_trellis_nt_m64's SK = 1 form";
+
 extern "C" {
 
-// r4d.h:416-419. SK, NP, U and skw are the reference's geometry knobs: accepted, not used.
+// r4d.h:416-419. Every element equals, bit for bit, what r4d_gemm_trellis_nt_m64 gives it at M = 64 with
+// SK = 1 and the same SKG (the same MFMA operands in the same order per K slice, the same slice order and
+// epilogue). SK must be 0 or 1 (0 means 1); NP, U and skw are the reference's geometry knobs: accepted, unused.
 void r4d_gemm_trellis_nt_m256(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
                               int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SK, int NP,
                               int SKG, int U, float out_scale, int64_t stream, int skw) {
-  (void)SK; (void)NP; (void)U; (void)skw;
+  (void)NP; (void)U; (void)skw;
+  if (SK != 0 && SK != 1) r4d::fail("gemm_trellis_nt_m256", sk_msg);
   m256_run(a0, a1, n_split, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale, stream,
            "gemm_trellis_nt_m256");
 }
 
 const char* r4d_gemm_trellis_nt_m256_check(int M, int K, int N, int n_split, int KB, int SK, int NP, int SKG,
                                            int U, int skw) {
-  (void)SK; (void)NP; (void)U; (void)skw;
+  (void)NP; (void)U; (void)skw;
+  if (SK != 0 && SK != 1) return r4d::check_result(sk_msg);
   return r4d::check_result(m256_check(M, K, N, n_split, KB, SKG));
 }
 

@@ -46,6 +46,41 @@ def test_m256_raw_full(KB, K, N, M, skg):
     assert np.array_equal(host_u16(full), O.epilogue_from_raw(raw_h, svh, out_scale))
 
 
+@pytest.mark.parametrize("M,K,N,KB,skg", [
+    (256, 1024, 384, 4, 1), (256, 2048, 256, 5, 2), (128, 1024, 256, 4, 4), (256, 5120, 256, 4, 10),
+    (256, 5120, 384, 3, 16), (128, 2560, 128, 5, 5), (256, 17408, 128, 4, 34),
+])
+def test_m256_bit_identical_to_m64_rows(M, K, N, KB, skg):
+    """r4d.h:402-412: every element of the M = 256 (128) launch equals, bit for bit, what the M <= 64 kernel
+    gives it at M = 64 with SK = 1 and the same SKG -- bf16 output and raw fp32 sums, one 64-row chunk at a
+    time; two A parts as well. SKG > 8 exercises the slice-sum order (8 interleaved runs)."""
+    banner("m256 == m64", M, K, N, KB, skg)
+    words, _, svh = WL.trellis_linear(K, N, KB, 3 * K + skg)
+    a = WL.activations_f16(M, K, 17, outlier_frac=0.01).view(np.uint16)
+    a1 = WL.activations_f16(M, K, 18).view(np.uint16)
+    w_d, a_d, a1_d, s_d = dev(words), dev(a), dev(a1), dev(svh)
+    ns = N // 2 if N % 256 == 0 else N
+    osc = float(np.float32(1.0 / np.sqrt(128.0)))
+    big = api.trellis_gemm_m256(a_d, w_d, s_d, K, N, KB, skg=skg, a1=a1_d, n_split=ns, out_scale=osc)
+    big_raw = api.trellis_gemm_m256(a_d, w_d, None, K, N, KB, skg=skg, a1=a1_d, n_split=ns, raw=True)
+    for r0 in range(0, M, 64):
+        sl = slice(r0, r0 + 64)
+        small = api.trellis_gemm_m64(a_d[sl].contiguous(), w_d, s_d, K, N, KB, skg=skg, a1=a1_d[sl].contiguous(),
+                                     n_split=ns, out_scale=osc, sk=1)
+        small_raw = api.trellis_gemm_m64(a_d[sl].contiguous(), w_d, None, K, N, KB, skg=skg,
+                                         a1=a1_d[sl].contiguous(), n_split=ns, raw=True, sk=1)
+        torch.cuda.synchronize()
+        assert torch.equal(big_raw[sl].view(torch.int32), small_raw.view(torch.int32)), r0
+        assert torch.equal(big[sl].view(torch.int16), small.view(torch.int16)), r0
+
+
+def test_m256_rejects_sk_above_1():
+    L = api.lib()
+    assert L.r4d_gemm_trellis_nt_m256_check(256, 1024, 256, 256, 4, 1, 0, 1, 0, 0) is None
+    msg = L.r4d_gemm_trellis_nt_m256_check(256, 1024, 256, 256, 4, 4, 0, 1, 0, 0)
+    assert msg and b"SK" in msg
+
+
 def test_m256_two_part():
     banner("m256 two-part")
     K, N, KB, M = 512, 512, 4, 256
