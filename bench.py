@@ -61,40 +61,55 @@ def main():
     copies = args.copies or max(2, int(np.ceil((1 << 30) / layer_wbytes)) + 1)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
-    lin = []
-    for i, (name, K, N) in enumerate(shapes):
-        nw = K * N * KB // 32
-        words = [torch.randint(-2**31, 2**31 - 1, (nw,), dtype=torch.int32, device=dev, generator=gen)
-                 for _ in range(copies)]
-        suh = torch.from_numpy(WL.signs(K, 10 + i)).to(dev)
-        svh = torch.from_numpy(WL.svh_scales(N, 20 + i)).to(dev)
-        x = torch.from_numpy(WL.activations_f16(M, K, 30 + i)).to(dev)
-        a = torch.empty((M, K), dtype=torch.float16, device=dev)
-        skg = api.trellis_gemv_skg(K, N, KB)
-        while (K // 128) % skg:     # whole 128-blocks per slice (the fused transform's rule)
-            skg -= 1
-        ws = torch.empty(max(1, skg * M * N), dtype=torch.float32, device=dev)
-        tickets = api.TicketBuffer(N, dev).t
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-        lin.append(dict(name=name, K=K, N=N, words=words, suh=suh, svh=svh, x=x, a=a, skg=skg, ws=ws,
-                        tickets=tickets, out=out))
+    # The engine's launches for one layer (src/model/linear.cpp ApplyLinear / SharedTrellisInput): the
+    # projections that read the same activations share one input-transform launch (nout = 2 or 3 outputs,
+    # kernels.h:110-128), and mlp.gate / mlp.up are the fused two-part linear mlp.gate_up
+    # (src/model/container.cpp:312; part 1 = up, from n_split = 17408, reads its own transform).
+    shape = {name: (K, N) for name, K, N in shapes}
+    lin, groups = [], []
+    for gi, (gname, members) in enumerate(WL.LAYER_GROUPS):
+        K = shape[members[0][0]][0]
+        x = torch.from_numpy(WL.activations_f16(M, K, 30 + gi)).to(dev)
+        g = dict(name=gname, x=x, suh=[], outs=[])
+        for li, parts in enumerate(members):
+            N = sum(shape[p][1] for p in parts)
+            nw = K * N * KB // 32
+            words = [torch.randint(-2**31, 2**31 - 1, (nw,), dtype=torch.int32, device=dev, generator=gen)
+                     for _ in range(copies)]
+            suh = [torch.from_numpy(WL.signs(K, 10 + 3 * gi + li + 7 * j)).to(dev) for j in range(len(parts))]
+            a = [torch.empty((M, K), dtype=torch.float16, device=dev) for _ in parts]
+            g["suh"] += suh
+            g["outs"] += a
+            svh = torch.from_numpy(WL.svh_scales(N, 20 + 3 * gi + li)).to(dev)
+            skg = api.trellis_gemv_skg(K, N, KB)
+            while (K // 128) % skg:     # whole 128-blocks per slice (the fused transform's rule)
+                skg -= 1
+            lin.append(dict(name="+".join(parts) if len(parts) > 1 else parts[0], K=K, N=N,
+                            n_split=shape[parts[0]][1] if len(parts) > 1 else N, words=words, suh=suh, svh=svh,
+                            x=x, a=a, skg=skg, ws=torch.empty(max(1, skg * M * N), dtype=torch.float32, device=dev),
+                            tickets=api.TicketBuffer(N, dev).t,
+                            out=torch.empty((M, N), dtype=torch.bfloat16, device=dev)))
+        groups.append(g)
     out_scale = float(np.float32(1.0 / np.sqrt(128.0)))
 
-    # Launches go to the current stream (the capture stream while a graph is being captured). The step is
-    # the engine's two launches per projection (input transform, then the GEMV on A); the fused entry
-    # (r4dx_trellis_gemv_xf: each workgroup transforms its own slice of x) is timed beside it.
+    # Launches go to the current stream (the capture stream while a graph is being captured). The step is the
+    # engine's launches for the layer: 6 input transforms and 9 GEMVs; the fused entry (r4dx_trellis_gemv_xf:
+    # each workgroup transforms its own slice of x; 9 launches) is timed beside it.
     def gemv(L, copy):
-        api.trellis_gemm_m64(L["a"], L["words"][copy], L["svh"], L["K"], L["N"], KB, skg=L["skg"],
+        api.trellis_gemm_m64(L["a"][0], L["words"][copy], L["svh"], L["K"], L["N"], KB, skg=L["skg"],
+                             a1=L["a"][1] if len(L["a"]) > 1 else None, n_split=L["n_split"],
                              out=L["out"], ws=L["ws"], tickets=L["tickets"], out_scale=out_scale)
 
     def gemv_xf(L, copy):
-        api.trellis_gemv_xf(L["x"], L["suh"], L["words"][copy], L["svh"], L["K"], L["N"], KB, skg=L["skg"],
+        api.trellis_gemv_xf(L["x"], L["suh"][0], L["words"][copy], L["svh"], L["K"], L["N"], KB, skg=L["skg"],
+                            suh1=L["suh"][1] if len(L["suh"]) > 1 else None, n_split=L["n_split"],
                             out=L["out"], ws=L["ws"], tickets=L["tickets"], out_scale=out_scale)
 
     def step(c, gemv_only=False):
+        if not gemv_only:
+            for g in groups:
+                api.trellis_input(g["x"], g["suh"], 0, bf16=False, outs=g["outs"])
         for L in lin:
-            if not gemv_only:
-                api.trellis_input(L["x"], [L["suh"]], 0, bf16=False, outs=[L["a"]])
             gemv(L, c)
 
     def step_fused(c):
@@ -172,7 +187,7 @@ def main():
         torch.cuda.synchronize()
         avg_ms = b0.elapsed_time(b1) / (R * copies)
         K, N = L["K"], L["N"]
-        ab = K * N * KB / 8 + M * K * 2 + M * N * 2 + 4 * N
+        ab = K * N * KB / 8 + len(L["a"]) * M * K * 2 + M * N * 2 + 4 * N
         gemv_ms += avg_ms
         alg_bytes += ab
         per_shape[L["name"]] = {"us": round(avg_ms * 1e3, 2), "GBs": round(ab / (avg_ms * 1e-3) / 1e9, 1)}
@@ -201,10 +216,12 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (uniform random trellis words, +-1 Hadamard signs, log-normal svh, N(0,1) x)",
-        "config": {"workload": f"config1: 10 projections of one 27B-class layer, M={M}, KB={KB}, "
+        "config": {"workload": f"config1: the 10 projections of one 27B-class layer as the engine launches them "
+                               f"(9 GEMVs: mlp.gate+up fused), M={M}, KB={KB}, "
                                f"{copies} rotating weight copies ({copies * layer_wbytes / 2**30:.2f} GiB)",
                    "M": M, "KB": KB, "weight_bytes_per_step": layer_wbytes,
-                   "step": "per projection: input transform + trellis GEMV (FWHT/svh epilogue, bf16 out)",
+                   "step": "6 input transforms (shared by projections with the same input, nout 1-3) + 9 trellis "
+                           "GEMVs (FWHT/svh epilogue, bf16 out)",
                    "fused_xf_ms_per_step": round(ms_step_fused, 4),
                    "fused_xf_GBs": round(layer_wbytes / (ms_step_fused * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

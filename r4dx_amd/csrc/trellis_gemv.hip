@@ -8,19 +8,17 @@
 // different pipes. Each wave streams one tile pair's k-range in 1 KiB steps (one dwordx4 per lane,
 // four (pair, k-tile) blocks at KB = 4), decodes its 32 weights per lane into four B fragments
 // (r4d_dev.h) and issues 4 x MT v_mfma_f32_16x16x32_f16 per step; at M <= 16 one row tile carries
-// the whole batch, so the MFMA cost per weight is independent of M up to 16. A workgroup is four
-// waves = four pairs = one 128-column FWHT group; SKG workgroups split K. Partial sums go to ws
-// [SKG][M][N] and the last workgroup of a group (ticket) sums them in slice order and finishes:
-// FWHT-128 in fp32 in the reference's stage order, * svh, * out_scale, one bf16 rounding. A row's
-// bits depend on (K, N, KB, SKG) only -- never on M or the other rows -- so decode rows equal verify
-// rows for every M <= 64 with the same SKG.
+// the whole batch, so the MFMA cost per weight is independent of M up to 16. SKG workgroups split K;
+// inside a workgroup, SK waves split each pair's slice (SK = 4, the split form) or one wave takes it
+// whole (SK = 1). Partial sums go to ws [SKG][M][N] and the last workgroup of a 128-column group
+// (ticket) sums them in a fixed order and finishes: FWHT-128 in fp32 in the reference's stage order,
+// * svh, * out_scale, one bf16 rounding. A row's bits depend on (K, N, KB, SKG, SK) only -- never on M,
+// on the pairs per workgroup or on the other rows -- so decode rows equal verify rows for every M <= 64.
 #include "r4d_dev.h"
 #include "r4d_host.h"
 #include "r4d_mi355x.h"
 
 namespace {
-
-constexpr int kWaves = 4;                      // pairs per workgroup = one 128-column group
 
 template <int KB>
 struct Words {
@@ -76,28 +74,29 @@ __device__ __forceinline__ void load_words_ptr(Words<KB>& s, const unsigned* __r
   for (int i = 0; i <= KB; ++i) s.w[i] = tile[r4_lane_word<KB>(c, i)];
 }
 
-// Kernel geometry: a workgroup is NPW tile pairs x SK waves (NPW SK = 4 waves, 256 threads); the
-// SK waves of a pair split the workgroup's K slice into SK contiguous parts, SKG workgroups split K.
-// NPW = 1 is the split form (every 128-column group is finished by the last of its 4 SKG
-// contributors through ws and tickets); NPW = 4 covers a whole group and, at SKG = 1, finishes it
-// in the workgroup (no ws). Many short workgroups let the dispatcher balance the VALU-bound decode
-// over the CUs (measured better on gfx950 than a persistent grid). Weights are prefetched PF steps
-// ahead (a step is 4 k-tiles = one dwordx4 per lane) and issued before A is staged in LDS.
+// Kernel geometry: a workgroup is NPW tile pairs x SK waves (64 NPW SK threads); the SK waves of a pair
+// split the workgroup's K slice into SK contiguous parts, added in k order; SKG workgroups split K.
+// The split form (SK = 4, NPW = 1 or 2) finishes every 128-column group in the last of its
+// SKG 4 / NPW contributors through ws and tickets; the whole-group form (NPW = 4, SK = 1) covers a group
+// and, at SKG = 1, finishes it in the workgroup (no ws). Many short workgroups let the dispatcher
+// balance the VALU-bound decode over the CUs (measured better on gfx950 than a persistent grid).
+// Weights are prefetched PF steps ahead (a step is 4 k-tiles = one dwordx4 per lane) and issued before
+// A is staged in LDS.
 constexpr int kRedParts = 8;         // the final slice sum is 8 interleaved runs, added in order
 constexpr int kRedRows = 4;          // rows of the final slice sum per pass
 
 // XF > 0: A0 is the raw input x [M][K] (XF 1: f16, 2: bf16) and the workgroup stages its own slice of the
 // transformed A = f16(FWHT128(fp32(x) * suh) * xscale) (suh0 / suh1 by column part) straight into LDS --
 // the arithmetic of r4dx_trellis_input_*, so A is bit-identical to the unfused path's.
-template <int KB, int MT, int NPW, bool ALDS, int XF>
-__global__ __launch_bounds__(256) void tq_gemv_kernel(
+template <int KB, int MT, int NPW, int SK, bool ALDS, int XF>
+__global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     const unsigned short* __restrict__ A0, const unsigned short* __restrict__ A1, int n_split,
     const unsigned* __restrict__ W, const float* __restrict__ svh, void* __restrict__ Cv,
     float* __restrict__ ws, unsigned* __restrict__ tickets, int M, int K, int N, int SKG, int full,
     float out_scale, const float* __restrict__ suh0, const float* __restrict__ suh1, float xscale) {
   constexpr int PF = 4;
-  constexpr int NT = 256;
-  constexpr int SK = 4 / NPW;
+  constexpr int NT = 64 * NPW * SK;
+  constexpr int NW = NPW * SK;                 // waves
   constexpr int BLK = 16 * KB;                 // words per (pair, k-tile) block
   extern __shared__ r4u4 lds_raw[];
   const int lane = threadIdx.x & 63;
@@ -199,7 +198,7 @@ __global__ __launch_bounds__(256) void tq_gemv_kernel(
   if constexpr (XF > 0) {
 #pragma unroll
     for (int j = 0; j < kXfPre; ++j) {
-      const int u = wave + 4 * j, b = u / M, r = u - b * M;
+      const int u = wave + NW * j, b = u / M, r = u - b * M;
       xpre[j][0] = xpre[j][1] = xpre[j][2] = xpre[j][3] = 0.f;
       if (u < xf_nblk * M && 8 * b < ktw) {
         const size_t kb = (size_t)16 * kt0 + 128 * (size_t)b;
@@ -366,25 +365,41 @@ __global__ __launch_bounds__(256) void tq_gemv_kernel(
     // Sum the SKG slices: run p (0..7) adds slices p, p + 8, ... in order; the 8 runs are then added
     // in order 0..7 -- the same arithmetic for every element whatever M is. kRedRows rows at a time
     // (bounded LDS); the finished sums land in red[r][128] for the epilogue.
-    const size_t sy = (size_t)M * N;
+    // SKG <= 64, so one batch of 8 loads (slices p, p + 8, ..., p + 56) covers a run. The loads are
+    // coherent (sc1) buffer loads over ws: a slice past SKG or an item past the end reads past the buffer
+    // and returns 0, so every thread issues all loads of its kFinItems items at once, with no branches.
+    const unsigned sy4 = (unsigned)M * (unsigned)N * 4u;
+    const r4_rsrc wsr = r4_make_rsrc(ws, (unsigned)SKG * sy4);
+    constexpr int kFinItems = 4;
     for (int r0 = 0; r0 < M; r0 += kRedRows) {
       const int rows = min(kRedRows, M - r0);
-      for (int idx = threadIdx.x; idx < kRedParts * rows * 128; idx += NT) {
-        const int p = idx / (rows * 128), e = idx - p * rows * 128;
-        const int r = r0 + (e >> 7), col = e & 127;
-        const float* src = ws + (size_t)r * N + n0 + col;
-        float v = 0.f;
-        for (int y = p; y < SKG; y += 8 * kRedParts) {
-          float tv[8];
+      const int items = kRedParts * rows * 128;
+      for (int b0 = 0; b0 < items; b0 += kFinItems * NT) {
+        float tv[kFinItems][8];
+#pragma unroll
+        for (int it = 0; it < kFinItems; ++it) {
+          const int idx = b0 + it * NT + (int)threadIdx.x;
+          const int p = idx / (rows * 128), e = idx - p * rows * 128;
+          const unsigned off = idx < items ? (unsigned)p * sy4 + ((unsigned)(r0 + (e >> 7)) * (unsigned)N + (unsigned)(n0 + (e & 127))) * 4u
+                                           : 0xFFFFFFF0u;
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
-            const int yy = y + u * kRedParts;
-            tv[u] = yy < SKG ? r4_load_coherent(src + (size_t)yy * sy) : 0.f;
+            const unsigned ou = off + (unsigned)u * (unsigned)kRedParts * sy4;
+            const unsigned o = (off == 0xFFFFFFF0u || ou < off) ? 0xFFFFFFF0u : ou;   // wrap-safe
+            tv[it][u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wsr, o, 0, 16));
           }
-#pragma unroll
-          for (int u = 0; u < 8; ++u) v += tv[u];
         }
-        runs[(size_t)p * kRedRows * 128 + e] = v;
+#pragma unroll
+        for (int it = 0; it < kFinItems; ++it) {
+          const int idx = b0 + it * NT + (int)threadIdx.x;
+          if (idx < items) {
+            const int p = idx / (rows * 128), e = idx - p * rows * 128;
+            float v = 0.f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += tv[it][u];
+            runs[(size_t)p * kRedRows * 128 + e] = v;
+          }
+        }
       }
       __syncthreads();
       for (int e = threadIdx.x; e < rows * 128; e += NT) {
@@ -400,7 +415,7 @@ __global__ __launch_bounds__(256) void tq_gemv_kernel(
   }
   // The epilogue: one wave per row, the group's 128 sums as (lane, lane + 64).
   const float sv0 = svh[n0 + lane], sv1 = svh[n0 + lane + 64];
-  for (int r = wave; r < M; r += 4) {
+  for (int r = wave; r < M; r += NW) {
     float v0 = red[r * 128 + lane], v1 = red[r * 128 + lane + 64];
     r4_fwht128_wave(v0, v1, lane);
     const float y0 = v0 * sv0, y1 = v1 * sv1;
@@ -441,8 +456,7 @@ __global__ __launch_bounds__(256) void tq_reconstruct_kernel(const unsigned* __r
 
 // Dynamic LDS of one launch.
 size_t gemv_ktl_pad(int SK, int ktw) { return (size_t)SK * ((((ktw + 3) >> 2) + SK - 1) / SK) * 4; }
-size_t gemv_lds(int MT, int NPW, bool alds, int ktw, int M) {
-  const int SK = 4 / NPW;
+size_t gemv_lds(int MT, int NPW, int SK, bool alds, int ktw, int M) {
   return (alds ? gemv_ktl_pad(SK, ktw) * M * 32 + 32 : 0) + (size_t)(SK - 1) * NPW * 8 * MT * 64 * 4 +
          (size_t)(M + kRedParts * kRedRows) * 128 * 4 + 16;
 }
@@ -450,46 +464,49 @@ constexpr size_t kAldsMax = 48 * 1024;   // A slices up to this many bytes are s
 
 constexpr size_t kXfAldsMax = 96 * 1024;   // the fused transform stages the slice in LDS up to this size
 
-template <int KB, int MT, int NPW, bool ALDS, int XF>
+template <int KB, int MT, int NPW, int SK, bool ALDS, int XF>
 void launch_gemv(const r4d_gemv_args& a) {
-  dim3 grid(a.N / 32 / NPW, a.SKG), block(256);
+  dim3 grid(a.N / 32 / NPW, a.SKG), block(64 * NPW * SK);
   const int ktw = a.K / 16 / a.SKG;
-  const size_t smem = gemv_lds(MT, NPW, ALDS, ktw, a.M);
+  const size_t smem = gemv_lds(MT, NPW, SK, ALDS, ktw, a.M);
   if (smem > 160 * 1024) r4d::fail("gemm_trellis_nt_m64", "LDS request above 160 KiB");
   static bool attr = false;
   if (!attr && smem > 64 * 1024) {
-    (void)hipFuncSetAttribute((const void*)tq_gemv_kernel<KB, MT, NPW, ALDS, XF>,
+    (void)hipFuncSetAttribute((const void*)tq_gemv_kernel<KB, MT, NPW, SK, ALDS, XF>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     attr = true;
   }
-  hipLaunchKernelGGL((tq_gemv_kernel<KB, MT, NPW, ALDS, XF>), grid, block, smem, (hipStream_t)a.stream,
+  hipLaunchKernelGGL((tq_gemv_kernel<KB, MT, NPW, SK, ALDS, XF>), grid, block, smem, (hipStream_t)a.stream,
                      (const unsigned short*)a.a0, (const unsigned short*)(a.a1 ? a.a1 : a.a0), a.n_split,
                      (const unsigned*)a.w, (const float*)a.svh, (void*)a.c, (float*)a.ws,
                      (unsigned*)a.tickets, a.M, a.K, a.N, a.SKG, a.full, a.out_scale, (const float*)a.suh0,
                      (const float*)(a.suh1 ? a.suh1 : a.suh0), a.xscale);
 }
 
-template <int KB, int MT, int NPW>
+template <int KB, int MT, int NPW, int SK>
 void launch_gemv_a(const r4d_gemv_args& a) {
   const int ktw = a.K / 16 / a.SKG;
-  const size_t abytes = gemv_ktl_pad(4 / NPW, ktw) * a.M * 32;
+  const size_t abytes = gemv_ktl_pad(SK, ktw) * a.M * 32;
   if (a.xf) {
     if (abytes > kXfAldsMax) r4d::fail("trellis_gemv_xf", "the A slice does not fit LDS: raise SKG");
-    if (a.xf == 2) launch_gemv<KB, MT, NPW, true, 2>(a);
-    else launch_gemv<KB, MT, NPW, true, 1>(a);
+    if (a.xf == 2) launch_gemv<KB, MT, NPW, SK, true, 2>(a);
+    else launch_gemv<KB, MT, NPW, SK, true, 1>(a);
   } else if (abytes <= kAldsMax) {
-    launch_gemv<KB, MT, NPW, true, 0>(a);
+    launch_gemv<KB, MT, NPW, SK, true, 0>(a);
   } else {
-    launch_gemv<KB, MT, NPW, false, 0>(a);
+    launch_gemv<KB, MT, NPW, SK, false, 0>(a);
   }
 }
 
 // The whole-group form (one wave per pair over the slice) at SK = 1 or for an unsplit launch without ws;
-// else the split form (one pair per workgroup, its slice split over 4 waves).
+// else the split form: each pair's slice split over 4 waves, one pair per workgroup at M = 1 and two at
+// M >= 2 (measured best; the pairs of a workgroup are independent, so the form does not change a bit,
+// and fewer workgroups take fewer tickets on the group's counter).
 template <int KB, int MT>
 void launch_gemv_np(const r4d_gemv_args& a) {
-  if (a.sk1 || (a.SKG == 1 && (a.ws == 0 || a.tickets == 0))) launch_gemv_a<KB, MT, 4>(a);
-  else launch_gemv_a<KB, MT, 1>(a);
+  if (a.sk1 || (a.SKG == 1 && (a.ws == 0 || a.tickets == 0))) launch_gemv_a<KB, MT, 4, 1>(a);
+  else if (a.M == 1) launch_gemv_a<KB, MT, 1, 4>(a);
+  else launch_gemv_a<KB, MT, 2, 4>(a);
 }
 
 template <int KB>
@@ -554,8 +571,8 @@ const char* r4dx_trellis_gemv_xf_check(int M, int K, int N, int n_split, int KB,
   std::string e;
   if ((K / 128) % SKG) e = "the fused transform needs whole 128-blocks per slice: (K / 128) % SKG == 0";
   else {
-    const int NPW = (SKG == 1 && !have_ws) ? 4 : 1;
-    if (gemv_ktl_pad(4 / NPW, K / 16 / SKG) * M * 32 > kXfAldsMax) e = "the A slice does not fit LDS: raise SKG";
+    const int SK = (SKG == 1 && !have_ws) ? 1 : 4;
+    if (gemv_ktl_pad(SK, K / 16 / SKG) * M * 32 > kXfAldsMax) e = "the A slice does not fit LDS: raise SKG";
   }
   return r4d::check_result(e);
 }
@@ -612,26 +629,23 @@ void r4d_trellis_reconstruct_f16(int64_t w, int64_t q, int K, int N, int KB, int
   r4d::launch_ok(entry);
 }
 
-// This build's split choice for the GEMV: a workgroup is one tile pair x 4 waves, each wave taking
-// whole 4-k-tile steps. SKG is picked among the divisors of K/16 (at most 32: the last workgroup of a
-// group sums the slices): first whole steps for every wave, then >= 4 steps per wave (the
-// per-workgroup setup and reduction amortised), then >= 1024 workgroups, then the most slices.
-// Independent of M, so every M <= 16 gets the same row bits.
+// This build's split choice for the GEMV, measured on MI355X over the 27B shapes (KB 4 and 5, M = 1 and
+// 8): the launch time is flat within a few per cent for 16..40 k-tiles per wave, so SKG is the divisor of
+// K/16 (2..32) that gives each of a slice's 4 waves closest to 28 k-tiles (log distance; ties to the
+// larger SKG). Independent of M, so every M <= 16 gets the same row bits.
 int r4d_mi355x_trellis_gemv_skg(int K, int N, int KB) {
   (void)KB;
-  const int KT = K / 16, pairs = N / 32;
-  if (KT <= 0 || pairs <= 0) return 1;
-  int best = 1, best_score = -1;
-  for (int d = 1; d <= 32 && d <= KT; ++d) {
+  const int KT = K / 16;
+  if (KT <= 0 || N <= 0) return 1;
+  int best = 1;
+  double best_d = 1e30;
+  for (int d = 2; d <= 32 && d <= KT; ++d) {
     if (KT % d) continue;
-    const int ktw = KT / d;
-    const int whole = ktw % 16 == 0;
-    const int steps = (ktw + 15) / 16;        // per wave
-    const long long wgs = (long long)pairs * d;
-    const int score = whole * 8 + (steps >= 4) * 4 + (wgs >= 1024) * 2 + (wgs >= 512);
-    if (score > best_score || (score == best_score && d > best)) {
+    const double per_wave = (double)KT / d / 4.0;
+    const double dist = per_wave > 28.0 ? per_wave / 28.0 : 28.0 / per_wave;
+    if (dist <= best_d) {
       best = d;
-      best_score = score;
+      best_d = dist;
     }
   }
   return best;

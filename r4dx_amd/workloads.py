@@ -18,6 +18,18 @@ LAYER_SHAPES = [
 ]
 
 
+# The engine's launch groups for those projections: (input group, linears); a linear with two names is a
+# fused two-part linear (part 1 from the first part's N on, reading its own input transform).
+LAYER_GROUPS = [
+    ("gdn.in", [("gdn.qkv",), ("gdn.z",)]),
+    ("gdn.out", [("gdn.out",)]),
+    ("attn.in", [("attn.q",), ("attn.k",), ("attn.v",)]),
+    ("attn.o", [("attn.o",)]),
+    ("mlp.in", [("mlp.gate", "mlp.up")]),
+    ("mlp.down", [("mlp.down",)]),
+]
+
+
 def trellis_words(K, N, KB, seed):
     rng = np.random.default_rng(seed)
     return rng.integers(0, 2**32, size=K * N * KB // 32, dtype=np.uint64).astype(np.uint32)
