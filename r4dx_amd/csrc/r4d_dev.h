@@ -40,6 +40,7 @@ typedef float r4f4 __attribute__((ext_vector_type(4)));
 typedef float r4f16 __attribute__((ext_vector_type(16)));
 typedef unsigned r4u4 __attribute__((ext_vector_type(4)));
 typedef unsigned r4u2 __attribute__((ext_vector_type(2)));
+typedef float r4f2 __attribute__((ext_vector_type(2)));
 typedef int r4i4 __attribute__((ext_vector_type(4)));
 
 #define R4_WAVE 64
@@ -183,6 +184,24 @@ __device__ __forceinline__ void r4_fwht128_wave(float& v0, float& v1, int lane) 
   const float a = v0, b = v1;
   v0 = a + b;
   v1 = a - b;
+}
+// The same transform with lane l holding elements 2 l (v0) and 2 l + 1 (v1): stage 0 pairs the two
+// registers, stage lg >= 1 pairs lane l with lane l ^ 2^(lg - 1). Every element sees the same fp32
+// operations in the same order as in r4_fwht128_wave.
+__device__ __forceinline__ void r4_fwht128_wave_pairs(float& v0, float& v1, int lane) {
+  {
+    const float a = v0, b = v1;
+    v0 = a + b;
+    v1 = a - b;
+  }
+#pragma unroll
+  for (int lg = 1; lg < 7; ++lg) {
+    const int hm = 1 << (lg - 1);
+    const float p0 = r4_xor_lane(v0, hm), p1 = r4_xor_lane(v1, hm);
+    const bool upper = (lane & hm) != 0;
+    v0 = upper ? p0 - v0 : v0 + p0;
+    v1 = upper ? p1 - v1 : v1 + p1;
+  }
 }
 
 // ---- misc ----------------------------------------------------------------------------------------

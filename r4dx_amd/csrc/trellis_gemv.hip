@@ -189,26 +189,31 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     }
   };
 
-  // Fused transform: the x and suh values of this wave's first (up to kXfPre) blocks are requested before
-  // the weight stream, so (loads completing in order) the transform does not wait behind the weights.
-  constexpr int kXfPre = 2;
-  float xpre[XF > 0 ? kXfPre : 1][4];
+  // Fused transform: one wave per (128-block, row) of the slice; lane l takes k = 128 b + 2 l, 2 l + 1 (one
+  // dword of x, two floats of suh). The x and suh of this wave's first kXfPre blocks are requested before
+  // the weight stream and the rest after it: loads retire in order, so a block requested after the
+  // weights waits for them.
+  constexpr int kXfPre = 6;
   const int xf_nblk = (ktl_pad + 7) >> 3;
   const float* __restrict__ suh_p = group * 128 >= n_split ? suh1 : suh0;
+  struct XfIn {
+    unsigned x2;   // x[2l], x[2l + 1] (f16 or bf16 bits)
+    r4f2 s2;       // suh[2l], suh[2l + 1]
+  };
+  auto xf_load = [&](int u) {
+    XfIn v = {0u, (r4f2){0.f, 0.f}};
+    const int b = u / M, r = u - b * M;
+    if (u < xf_nblk * M && 8 * b < ktw) {
+      const size_t kb = (size_t)16 * kt0 + 128 * (size_t)b + 2 * lane;
+      v.x2 = *(const unsigned*)(A0 + (size_t)r * K + kb);
+      v.s2 = *(const r4f2*)(suh_p + kb);
+    }
+    return v;
+  };
+  XfIn xpre[XF > 0 ? kXfPre : 1];
   if constexpr (XF > 0) {
 #pragma unroll
-    for (int j = 0; j < kXfPre; ++j) {
-      const int u = wave + NW * j, b = u / M, r = u - b * M;
-      xpre[j][0] = xpre[j][1] = xpre[j][2] = xpre[j][3] = 0.f;
-      if (u < xf_nblk * M && 8 * b < ktw) {
-        const size_t kb = (size_t)16 * kt0 + 128 * (size_t)b;
-        const unsigned short* xr = A0 + (size_t)r * K + kb;
-        xpre[j][0] = XF == 2 ? r4_bf16_to_f32(xr[lane]) : r4_f16_to_f32(xr[lane]);
-        xpre[j][1] = XF == 2 ? r4_bf16_to_f32(xr[lane + 64]) : r4_f16_to_f32(xr[lane + 64]);
-        xpre[j][2] = suh_p[kb + lane];
-        xpre[j][3] = suh_p[kb + 64 + lane];
-      }
-    }
+    for (int j = 0; j < kXfPre; ++j) xpre[j] = xf_load(wave + NW * j);
   }
   // The weight stream starts before A is staged, so its latency overlaps the staging.
   St ring[PF];
@@ -217,45 +222,31 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     for (int i = 0; i < PF; ++i) load(ring[i], i);
   }
   if constexpr (ALDS && XF > 0) {
-    // one wave per (128-block, row) of the slice: lane l transforms k = 128 b + l and + 64, and writes
-    // each f16 to its fragment slot -- element k16 of k-tile ktl sits at half (k16 >> 3) + 2 ((k16 >> 2)
-    // & 1) of the 32-byte (ktl, row) chunk (h = 0: k 0-3, 8-11; h = 1: k 4-7, 12-15); then the zero block.
-    unsigned short* ah = (unsigned short*)alds;
-    const int nblk = xf_nblk;
-#pragma unroll 1
-    for (int u = wave, j = 0; u < nblk * M; u += NT / 64, ++j) {
+    // A = f16(FWHT128(fp32(x) * suh) * xscale) (r4_fwht128_wave_pairs: the same fp32 operations per element
+    // as r4dx_trellis_input_*), each lane's two adjacent k written as one dword to its fragment slot --
+    // element k16 of k-tile ktl sits at half (k16 >> 3) + 2 ((k16 >> 2) & 1) of the 32-byte (ktl, row)
+    // chunk (h = 0: k 0-3, 8-11; h = 1: k 4-7, 12-15); then the zero block.
+    unsigned* ah = (unsigned*)alds;
+    auto xf_stage = [&](int u, const XfIn& v) {
       const int b = u / M, r = u - b * M;
-      unsigned short hv[2] = {0, 0};
+      if (u >= xf_nblk * M) return;
+      unsigned hv = 0u;
       if (8 * b < ktw) {
-        float x0, x1, s0, s1;
-        if (j < kXfPre) {
-          // (a constant index per unrolled copy is not needed: the preload array is tiny)
-          x0 = xpre[0][0]; x1 = xpre[0][1]; s0 = xpre[0][2]; s1 = xpre[0][3];
-#pragma unroll
-          for (int jj = 1; jj < kXfPre; ++jj)
-            if (j == jj) { x0 = xpre[jj][0]; x1 = xpre[jj][1]; s0 = xpre[jj][2]; s1 = xpre[jj][3]; }
-        } else {
-          const size_t kb = (size_t)16 * kt0 + 128 * (size_t)b;
-          const unsigned short* xr = A0 + (size_t)r * K + kb;
-          x0 = XF == 2 ? r4_bf16_to_f32(xr[lane]) : r4_f16_to_f32(xr[lane]);
-          x1 = XF == 2 ? r4_bf16_to_f32(xr[lane + 64]) : r4_f16_to_f32(xr[lane + 64]);
-          s0 = suh_p[kb + lane];
-          s1 = suh_p[kb + 64 + lane];
-        }
-        float v0 = x0 * s0;
-        float v1 = x1 * s1;
-        r4_fwht128_wave(v0, v1, lane);
-        hv[0] = r4_f16_rn(v0 * xscale);
-        hv[1] = r4_f16_rn(v1 * xscale);
+        const float x0 = XF == 2 ? r4_bf16_to_f32((unsigned short)(v.x2 & 0xFFFFu)) : r4_f16_to_f32((unsigned short)(v.x2 & 0xFFFFu));
+        const float x1 = XF == 2 ? r4_bf16_to_f32((unsigned short)(v.x2 >> 16)) : r4_f16_to_f32((unsigned short)(v.x2 >> 16));
+        float v0 = x0 * v.s2[0];
+        float v1 = x1 * v.s2[1];
+        r4_fwht128_wave_pairs(v0, v1, lane);
+        hv = (unsigned)r4_f16_rn(v0 * xscale) | ((unsigned)r4_f16_rn(v1 * xscale) << 16);
       }
+      const int kl = 128 * b + 2 * lane, ktl = kl >> 4, k16 = kl & 15;
+      if (ktl < ktl_pad) ah[(size_t)(ktl * M + r) * 8 + (((k16 >> 3) & 1) + 2 * ((k16 >> 2) & 1)) * 2 + ((k16 & 3) >> 1)] = hv;
+    };
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int kl = 128 * b + lane + 64 * e, ktl = kl >> 4, k16 = kl & 15;
-        if (ktl < ktl_pad)
-          ah[(size_t)(ktl * M + r) * 16 + (((k16 >> 3) & 1) + 2 * ((k16 >> 2) & 1)) * 4 + (k16 & 3)] = hv[e];
-      }
-    }
-    if (threadIdx.x < 16) ah[(size_t)ktl_pad * M * 16 + threadIdx.x] = 0;
+    for (int j = 0; j < kXfPre; ++j) xf_stage(wave + NW * j, xpre[j]);
+#pragma unroll 1
+    for (int u = wave + NW * kXfPre; u < xf_nblk * M; u += NW) xf_stage(u, xf_load(u));
+    if (threadIdx.x < 8) ah[(size_t)ktl_pad * M * 8 + threadIdx.x] = 0u;
     __syncthreads();
   } else if constexpr (ALDS) {
     // chunk (ktl, row, j): k 16 (kt0 + ktl) + 8j .. + 8 of A[row] -> halves of fragments h = 0, 1;
@@ -278,6 +269,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
       for (int i = 0; i < PF; ++i) {
         compute(ring[i], st + i);
         load(ring[i], st + i + PF);
+        __builtin_amdgcn_sched_barrier(0);   // one step at a time: no decode hoisted across the reload
       }
     }
 #pragma unroll
