@@ -285,22 +285,47 @@ __global__ __launch_bounds__(256) void tq_m256_finish(const float* __restrict__ 
   const int n0 = group * 128;
   const size_t sy = (size_t)M * N;
   // the M <= 64 kernel's slice order: run p (0..7) = 0.f + slices p, p + 8, ... in order, then the 8 runs
-  // added in order 0..7
+  // added in order 0..7. Up to 8 slices (one per run), each thread requests all slices of 8 of its rows
+  // at once (buffer loads: a slice past SKG reads past the buffer and returns 0, which is exactly what an
+  // empty run adds); more slices take the general loop.
   float v[16];
-#pragma unroll 1
-  for (int p = 0; p < 8; ++p) {
-    float run[16];
+  if (SKG <= 8) {
+    const unsigned sy4 = (unsigned)sy * 4u;
+    const r4_rsrc wr = mk_rsrc(ws, (unsigned)SKG * sy4);
 #pragma unroll
-    for (int u = 0; u < 16; ++u) run[u] = 0.f;
-    for (int y = p; y < SKG; y += 8) {
-      float t[16];
+    for (int h = 0; h < 2; ++h) {
+      float t[8][8];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) t[u] = ws[(size_t)y * sy + (size_t)(r0 + rh + 2 * u) * N + n0 + col];
+      for (int p = 0; p < 8; ++p)
 #pragma unroll
-      for (int u = 0; u < 16; ++u) run[u] += t[u];
+        for (int u = 0; u < 8; ++u) {
+          const unsigned off = (unsigned)p * sy4 + (unsigned)((r0 + rh + 2 * (8 * h + u)) * N + n0 + col) * 4u;
+          t[p][u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0));
+        }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        float acc = 0.f + t[0][u];
+#pragma unroll
+        for (int p = 1; p < 8; ++p) acc = acc + (0.f + t[p][u]);
+        v[8 * h + u] = acc;
+      }
     }
+  } else {
+#pragma unroll 1
+    for (int p = 0; p < 8; ++p) {
+      float run[16];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) v[u] = p == 0 ? run[u] : v[u] + run[u];
+      for (int u = 0; u < 16; ++u) run[u] = 0.f;
+      for (int y = p; y < SKG; y += 8) {
+        float t[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) t[u] = ws[(size_t)y * sy + (size_t)(r0 + rh + 2 * u) * N + n0 + col];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) run[u] += t[u];
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = p == 0 ? run[u] : v[u] + run[u];
+    }
   }
   if (!full) {
     float* Cf = (float*)Cv;
