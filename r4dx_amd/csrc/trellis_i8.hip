@@ -173,21 +173,34 @@ struct TI8Args {
   float* ws;
   int K, N, SKG;
   float out_scale;
+  // stream-K (G > 0): G workgroups share the U = (N / 128) (K / 128) (column group, 128-k block) units
+  // evenly; partial pieces of a group go to ws slot 2 c + (first group of c ? 0 : 1) and the last piece to
+  // arrive (ticket) adds all of them in piece order, then finishes the group
+  int G, U;
+  unsigned* tickets;
 };
+constexpr int kStreamG = 256;                   // workgroups of a stream-K launch (one per CU)
+constexpr int kSlot = 256 * 128;                // values per partial piece
 
 // the B stage's column slot: bit 3 flipped on odd 16-column tiles (a decode lane writes columns 16 t + 8 cs +
 // c of its pair: the t = 0 and t = 1 lanes of one write then use different banks)
 __device__ __forceinline__ int ti8_bslot(int n) { return n ^ (((n >> 4) & 1) << 3); }
 
+// the last workgroup c whose stream-K range [floor(c U / G), ...) starts at or before unit x
+__device__ __forceinline__ int ti8_unit_owner(int x, int U, int G) {
+  return (int)((((long long)x + 1) * G + U - 1) / U) - 1;
+}
+
+// One piece: column group `group`, k-tiles kt0 .. kt0 + 4 nst of it. slot < 0: the whole group's K range
+// (or a classic split slice ky); slot >= 0: a stream-K partial piece (see TI8Args).
 template <int KB, int SC, int OUT, bool DENSE>
-__global__ __launch_bounds__(512, 1) void ti8_gemm_kernel(TI8Args p) {
+__device__ __forceinline__ void ti8_piece(const TI8Args& p, unsigned char (*bst)[4][128][16], int* flag, int group,
+                                          int ky, int kt0, int nst, int slot) {
   constexpr bool BLKA = SC != kSCoarse;           // per-128 activation scales: fp32 accumulators
-  __shared__ __attribute__((aligned(16))) unsigned char bst[2][4][128][16];   // [stage][k-tile][column slot][16 B]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int group = blockIdx.x, ky = blockIdx.y;
   const int K = p.K, N = p.N, KT = K >> 4;
-  const int ktw = KT / p.SKG, kt0 = ky * ktw, nst = ktw >> 2;
+  const int ktw = 4 * nst;
   const int n0 = group * 128;
   const int part = (p.a8[1] != nullptr && n0 >= p.n_split) ? 1 : 0;
   const int g = lane >> 4, r16 = lane & 15;
@@ -341,6 +354,72 @@ __global__ __launch_bounds__(512, 1) void ti8_gemm_kernel(TI8Args p) {
   for (int i = 0; i < PF - 1; ++i)
     if (st + i < nst) step(ring[i], st + i, (i & 1) != 0);
 
+  // ---- stream-K partial piece (dense launches only): store it, take the group's ticket; the last piece adds
+  // all pieces in order
+  if (DENSE && slot >= 0) {
+    const int nb = K >> 7;
+    const int c_lo = ti8_unit_owner(group * nb, p.U, p.G), c_hi = ti8_unit_owner((group + 1) * nb - 1, p.U, p.G);
+    auto slot_of = [&](int c) {
+      const int first = (int)((long long)c * p.U / p.G) / nb;
+      return 2 * c + (group == first ? 0 : 1);
+    };
+    // int32 pieces (coarse) and fp32 pieces (per-128) each through their own typed path
+    auto idx = [&](int ii, int ct, int j) { return (((wave * 2 + ii) * 8 + ct) * 4 + j) * 64 + lane; };
+    if constexpr (BLKA) {
+      float* dst = p.ws + (size_t)slot * kSlot;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) r4_store_coherent(&dst[idx(ii, ct, j)], facc[ii][ct][j]);
+    } else {
+      int* dst = (int*)p.ws + (size_t)slot * kSlot;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            __hip_atomic_store(&dst[idx(ii, ct, j)], iacc[ii][ct][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!r4_ticket_last(&p.tickets[group], (unsigned)(c_hi - c_lo + 1), flag)) return;
+    for (int c = c_lo; c <= c_hi; ++c) {
+      if constexpr (BLKA) {
+        const float* src = p.ws + (size_t)slot_of(c) * kSlot;
+        float t[2][8][4];
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) t[ii][ct][j] = r4_load_coherent(&src[idx(ii, ct, j)]);
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) facc[ii][ct][j] = c == c_lo ? t[ii][ct][j] : facc[ii][ct][j] + t[ii][ct][j];
+      } else {
+        const int* src = (const int*)p.ws + (size_t)slot_of(c) * kSlot;
+        int t[2][8][4];
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              t[ii][ct][j] = __hip_atomic_load(&src[idx(ii, ct, j)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) iacc[ii][ct][j] = (c == c_lo ? 0 : iacc[ii][ct][j]) + t[ii][ct][j];
+      }
+    }
+  }
+
   // ---- this slice's values: rows 32 w + 16 ii + 4 g + j, column n0 + 16 ct + r16
   if constexpr (OUT == kOutI32) {
     if (p.SKG > 1) {
@@ -442,6 +521,27 @@ __global__ __launch_bounds__(512, 1) void ti8_gemm_kernel(TI8Args p) {
   }
 }
 
+template <int KB, int SC, int OUT, bool DENSE>
+__global__ __launch_bounds__(512, 1) void ti8_gemm_kernel(TI8Args p) {
+  __shared__ __attribute__((aligned(16))) unsigned char bst[2][4][128][16];   // [stage][k-tile][column slot][16 B]
+  __shared__ int flag;
+  if (!DENSE || p.G == 0) {
+    const int ktw = (p.K >> 4) / p.SKG;
+    ti8_piece<KB, SC, OUT, DENSE>(p, bst, &flag, blockIdx.x, blockIdx.y, blockIdx.y * ktw, ktw >> 2, -1);
+    return;
+  }
+  // stream-K: this workgroup's units [u0, u1), a unit = (group, 128-k block) = 2 steps
+  const int c = blockIdx.x, nb = p.K >> 7;
+  const int u0 = (int)((long long)c * p.U / p.G), u1 = (int)((long long)(c + 1) * p.U / p.G);
+  const int first = u0 / nb;
+  for (int g = first; g * nb < u1; ++g) {
+    const int b0 = max(u0, g * nb) - g * nb, b1 = min(u1, (g + 1) * nb) - g * nb;
+    const bool whole = b0 == 0 && b1 == nb;
+    ti8_piece<KB, SC, OUT, DENSE>(p, bst, &flag, g, 0, 8 * b0, 2 * (b1 - b0), whole ? -1 : 2 * c + (g == first ? 0 : 1));
+    __syncthreads();   // the next piece restages the LDS
+  }
+}
+
 // The second pass of a split dense launch: the SKG slices of ws added in slice order (as integers for the
 // int32 test entry), then stored as f16 (or int32).
 template <int OUT>
@@ -476,7 +576,8 @@ std::string ti8_check(int M, int K, int N, int n_split, int KB, int skw, int skg
 
 template <int KB, int SC, int OUT, bool DENSE>
 void ti8_launch(const TI8Args& a, int N, int SKG, hipStream_t st) {
-  hipLaunchKernelGGL((ti8_gemm_kernel<KB, SC, OUT, DENSE>), dim3(N / 128, SKG), dim3(512), 0, st, a);
+  if (a.G > 0) hipLaunchKernelGGL((ti8_gemm_kernel<KB, SC, OUT, DENSE>), dim3(a.G), dim3(512), 0, st, a);
+  else hipLaunchKernelGGL((ti8_gemm_kernel<KB, SC, OUT, DENSE>), dim3(N / 128, SKG), dim3(512), 0, st, a);
 }
 
 void ti8_run(bool p128, int64_t a8_0, int64_t sa_0, int64_t a8_1, int64_t sa_1, int n_split, int64_t w, int64_t sw,
@@ -559,17 +660,18 @@ std::string dense_check(int M, int K, int N, int SKG) {
   if (M != 256) return "M must be 256 (the prefill chunk)";
   if (K <= 0 || N <= 0 || K % 128 || N % 128) return "K and N must be positive multiples of 128";
   if ((long long)N * K >= (1LL << 32)) return "N K must be below 2^32 bytes";
-  if (SKG < 1 || SKG > 64 || (K / 128) % SKG) return "SKG must be 1..64 and divide K / 128";
+  if (SKG < 0 || SKG > 64 || (SKG > 0 && (K / 128) % SKG)) return "SKG must be 0 (stream-K) or 1..64 dividing K / 128";
   return "";
 }
 
-void dense_run(int64_t a8, int64_t sa, int64_t w8, int64_t sw, int64_t c, int64_t ws, int M, int K, int N, int SKG,
-               int scale_mode, bool raw_i32, int64_t stream, const char* entry) {
+void dense_run(int64_t a8, int64_t sa, int64_t w8, int64_t sw, int64_t c, int64_t ws, int64_t tickets, int M, int K,
+               int N, int SKG, int scale_mode, bool raw_i32, int64_t stream, const char* entry) {
   r4d::require(entry, dense_check(M, K, N, SKG));
   if (scale_mode < 0 || scale_mode > 2) r4d::fail(entry, "scale_mode must be 0 (row / column), 1 (per-128 "
                                                          "activation, column weight) or 2 (per-128 both)");
   if (!a8 || !w8 || !c || (!raw_i32 && (!sa || !sw))) r4d::fail(entry, "null buffer");
   if (SKG > 1 && !ws) r4d::fail(entry, "a split launch (SKG > 1) needs ws");
+  if (SKG == 0 && (!ws || !tickets)) r4d::fail(entry, "a stream-K launch (SKG = 0) needs ws and tickets");
   TI8Args a{};
   a.a8[0] = (const signed char*)a8;
   a.sa[0] = a.sa[1] = (const float*)sa;
@@ -580,8 +682,13 @@ void dense_run(int64_t a8, int64_t sa, int64_t w8, int64_t sw, int64_t c, int64_
   a.ws = (float*)ws;
   a.K = K;
   a.N = N;
-  a.SKG = SKG;
+  a.SKG = SKG == 0 ? 1 : SKG;
   a.out_scale = 1.f;
+  if (SKG == 0) {
+    a.U = (N / 128) * (K / 128);
+    a.G = a.U < kStreamG ? a.U : kStreamG;
+    a.tickets = (unsigned*)tickets;
+  }
   hipStream_t st = (hipStream_t)stream;
   if (raw_i32) ti8_launch<4, kSCoarse, kOutI32, true>(a, N, SKG, st);
   else if (scale_mode == 0) ti8_launch<4, kSCoarse, kOutF16, true>(a, N, SKG, st);
@@ -604,21 +711,24 @@ void dense_run(int64_t a8, int64_t sa, int64_t w8, int64_t sw, int64_t c, int64_
 extern "C" {
 
 const char* r4d_gemm_i8_dense_check(int M, int K, int N, int SKG) { return r4d::check_result(dense_check(M, K, N, SKG)); }
-size_t r4d_gemm_i8_dense_ws_bytes(int M, int N, int SKG) { return SKG > 1 ? (size_t)SKG * M * N * 4 : 0; }
+size_t r4d_gemm_i8_dense_ws_bytes(int M, int N, int SKG) {
+  if (SKG == 0) return (size_t)kStreamG * 2 * kSlot * 4;   // stream-K: two partial-piece slots per workgroup
+  return SKG > 1 ? (size_t)SKG * M * N * 4 : 0;
+}
 // The dense int8 GEMM: a8 in the A8 layout (r4d_trellis_i8_quant_act / _row), w8 in the W8 block layout
 // (r4d_i8_pack_w), C f16 [256][N]. scale_mode 0: sa [256], sw [N]; 1: sa [K/128][256], sw [N]; 2: sa
-// [K/128][256], sw [K/128][N]. SKG > 1: ws (ws_bytes); tickets accepted and unused.
+// [K/128][256], sw [K/128][N]. SKG > 1: K split into SKG slices (ws, a second pass adds them); SKG = 0:
+// stream-K over 256 workgroups (ws ws_bytes(M, N, 0), tickets u32 [N/128] zero before the first call and
+// self-resetting; int32 sums are exact in any order, the per-128 modes add pieces in a fixed order).
 void r4d_gemm_i8_dense(int64_t a8, int64_t sa, int64_t w8, int64_t sw, int64_t c, int64_t ws, int64_t tickets, int M,
                        int K, int N, int SKG, int scale_mode, int64_t stream) {
-  (void)tickets;
-  dense_run(a8, sa, w8, sw, c, ws, M, K, N, SKG, scale_mode, false, stream, "gemm_i8_dense");
+  dense_run(a8, sa, w8, sw, c, ws, tickets, M, K, N, SKG, scale_mode, false, stream, "gemm_i8_dense");
 }
 // Test entry: the exact int32 sums C[m][n] = sum_k A[m][k] W[n][k] (int32 [256][N]) through the same kernel and
 // split.
 void r4d_gemm_i8_dense_raw(int64_t a8, int64_t w8, int64_t c, int64_t ws, int64_t tickets, int M, int K, int N,
                            int SKG, int64_t stream) {
-  (void)tickets;
-  dense_run(a8, 0, w8, 0, c, ws, M, K, N, SKG, 0, true, stream, "gemm_i8_dense_raw");
+  dense_run(a8, 0, w8, 0, c, ws, tickets, M, K, N, SKG, 0, true, stream, "gemm_i8_dense_raw");
 }
 // This build's K split for the dense int8 GEMM: the fewest slices (of at least 1024 k) that reach 128
 // workgroups -- the split that measured fastest at both config-4 shapes (1 at 5120 x 17408, 4 at 17408 x 5120).

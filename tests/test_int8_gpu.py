@@ -73,8 +73,11 @@ def _i32_ref(a, w):
 
 
 @pytest.mark.parametrize("K,N,skg", [(128, 128, 1), (512, 256, 1), (1024, 384, 2), (2048, 128, 4), (640, 512, 5),
-                                     (384, 256, 3)])
+                                     (384, 256, 3), (128, 128, 0), (1024, 384, 0), (640, 512, 0), (5120, 1280, 0),
+                                     (2048, 4352, 0)])
 def test_dense_int32_exact(K, N, skg):
+    """skg = 0 is stream-K: 256 workgroups share the (group, 128-k block) units, so groups split into pieces
+    at any block and workgroups span group boundaries; the int32 sums stay exact."""
     banner("i8 raw", K, N, skg)
     rng = np.random.default_rng(K + N)
     a = rng.integers(-127, 128, (256, K)).astype(np.int8)
@@ -113,7 +116,7 @@ def _oracle_mode(x, w8, sw, mode):
 
 
 @pytest.mark.parametrize("mode", [0, 1, 2])
-@pytest.mark.parametrize("K,N,skg", [(1024, 256, 1), (2048, 384, 2), (1536, 128, 3)])
+@pytest.mark.parametrize("K,N,skg", [(1024, 256, 1), (2048, 384, 2), (1536, 128, 3), (2048, 384, 0), (5120, 2176, 0)])
 def test_dense_scaled(mode, K, N, skg):
     banner("i8 dense", mode, K, N, skg)
     x, w8, sw = WL.int8_case(K, N, 7)
@@ -123,6 +126,20 @@ def test_dense_scaled(mode, K, N, skg):
     c = api.i8_dense_gemm(a8, sa, api.i8_pack_w(dev(w8)), dev(sw.reshape(-1)), K, N, scale_mode=mode, skg=skg)
     torch.cuda.synchronize()
     assert close_rel(c.float().cpu().numpy(), _oracle_mode(x, w8, sw, mode), 1e-3, 1e-4) <= 1.0
+
+
+def test_dense_stream_repeat_identical():
+    """Stream-K, per-128 scales (fp32 pieces): the pieces are added in a fixed order, so repeats are byte-identical."""
+    K, N = 5120, 2176
+    x, w8, sw = WL.int8_case(K, N, 9)
+    a8, sa = api.i8_quant(dev(x.view(np.uint16)), True)
+    w_d, sw_d = api.i8_pack_w(dev(w8)), dev(sw)
+    work = api.I8Workspace(N, 0, w_d.device)
+    c0 = api.i8_dense_gemm(a8, sa, w_d, sw_d, K, N, scale_mode=1, skg=0, work=work)
+    for _ in range(3):
+        c = api.i8_dense_gemm(a8, sa, w_d, sw_d, K, N, scale_mode=1, skg=0, work=work)
+        torch.cuda.synchronize()
+        assert torch.equal(c.view(torch.int16), c0.view(torch.int16))
 
 
 @pytest.mark.parametrize("K,N", [(5120, 17408), (17408, 5120)])
