@@ -169,8 +169,21 @@ __device__ __forceinline__ int r4_lane_word(int c, int i) {
 // each pair (i, i + 2^lg) -> (a + b, a - b) in fp32 (reference order: tests/kernels/trellis_ref.hpp:
 // 120-131): for lg < 6 the partner is lane l ^ 2^lg and the lower index keeps a + b, the upper takes
 // a - b (= partner - own); lg = 6 pairs the two registers.
+// v of lane l ^ mask (mask a power of two below 64, a compile-time constant after unrolling). Masks 1-8 are
+// DPP moves inside a row of 16 lanes (ALU latency; 4 and 8 as two mirrors: (l ^ 7) ^ 3 = l ^ 4, (l ^ 15) ^ 7
+// = l ^ 8), 16 a ds_swizzle inside 32 lanes, 32 a ds_bpermute. Pure data movement: the values are unchanged.
+__device__ __forceinline__ int r4_xor_lane_i(int v, int mask) {
+  switch (mask) {
+    case 1: return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);     // quad_perm [1, 0, 3, 2]
+    case 2: return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);     // quad_perm [2, 3, 0, 1]
+    case 4: return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true), 0x1B, 0xF, 0xF, true);
+    case 8: return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true), 0x141, 0xF, 0xF, true);
+    case 16: return __builtin_amdgcn_ds_swizzle(v, (16 << 10) | 0x1F);  // bit mode, xor 16 inside 32 lanes
+    default: return __shfl_xor(v, mask, R4_WAVE);
+  }
+}
 __device__ __forceinline__ float r4_xor_lane(float v, int mask) {
-  return __shfl_xor(v, mask, R4_WAVE);
+  return __builtin_bit_cast(float, r4_xor_lane_i(__builtin_bit_cast(int, v), mask));
 }
 __device__ __forceinline__ void r4_fwht128_wave(float& v0, float& v1, int lane) {
 #pragma unroll

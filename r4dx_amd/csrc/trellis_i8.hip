@@ -497,7 +497,7 @@ __device__ __forceinline__ void ti8_piece(const TI8Args& p, unsigned char (*bst)
             const bool upper = (lane & mask) != 0;
 #pragma unroll
             for (int ct = 0; ct < 8; ++ct) {
-              const float o = __shfl_xor(x[ct], mask, 64);
+              const float o = r4_xor_lane(x[ct], mask);
               x[ct] = upper ? o - x[ct] : x[ct] + o;
             }
           }

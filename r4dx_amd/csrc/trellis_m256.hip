@@ -223,7 +223,7 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
       for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float o = __shfl_xor(acc[i][ct][j], mask, 64);
+          const float o = r4_xor_lane(acc[i][ct][j], mask);
           acc[i][ct][j] = upper ? o - acc[i][ct][j] : acc[i][ct][j] + o;
         }
     };
