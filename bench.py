@@ -37,6 +37,9 @@ def parse():
     ap.add_argument("--no-m256", action="store_true", help="skip the M = 256 prefill GEMM leg")
     ap.add_argument("--no-w4", action="store_true", help="skip the w4a16 LM-head leg")
     ap.add_argument("--no-i8", action="store_true", help="skip the int8 prefill GEMM legs")
+    ap.add_argument("--pmc-prefill", action="store_true",
+                    help="counter pass for the prefill kernels: each config-2 M = 256 shape, then the config-4 "
+                         "dense and trellis int8 GEMMs, launched twice each; prints the launch order, no JSON line")
     ap.add_argument("--pmc", action="store_true",
                     help="counter pass for rocprofv3 --pmc: a 512 MiB copy (calibration) and two eager "
                          "passes of the GEMV launches; prints no JSON line")
@@ -55,6 +58,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.pmc_prefill:
+        pmc_prefill(api, WL, args.kb)
+        return
     KB, M = args.kb, args.m
     shapes = WL.LAYER_SHAPES
     layer_wbytes = sum(K * N * KB // 8 for _, K, N in shapes)
@@ -236,6 +242,38 @@ def main():
         "wall_s": round(wall, 3),
     }
     print(json.dumps(line), flush=True)
+
+
+def pmc_prefill(api, WL, KB):
+    """Eager launches of the prefill kernels for a counter pass (MFMA busy cycles per dispatch): every config-2
+    shape through r4d_gemm_trellis_nt_m256, then config 4 through the dense int8 GEMM (row scales) and the
+    trellis int8 GEMM (coarse), each twice. Prints the launch order with the algorithmic ops per launch."""
+    import numpy as np
+    import torch
+    dev = torch.device("cuda:0")
+    order = []
+    for i, (name, K, N) in enumerate(WL.LAYER_SHAPES):
+        words = torch.randint(-2**31, 2**31 - 1, (K * N * KB // 32,), dtype=torch.int32, device=dev)
+        a = torch.from_numpy(WL.activations_f16(256, K, 40 + i, outlier_frac=0.01)).to(dev)
+        svh = torch.from_numpy(WL.svh_scales(N, 50 + i)).to(dev)
+        for _ in range(2):
+            api.trellis_gemm_m256(a, words, svh, K, N, KB, out_scale=0.08838834764831845)
+        order.append(["tq_m256_kernel", name, K, N, 2 * 256 * K * N])
+    for K, N in ((5120, 17408), (17408, 5120)):
+        x, w8, sw = WL.int8_case(K, N, 3)
+        w_d, sw_d = api.i8_pack_w(torch.from_numpy(w8).to(dev)), torch.from_numpy(sw).to(dev)
+        a8, sa = api.i8_quant(torch.from_numpy(x.view(np.uint16)).to(dev), False)
+        for _ in range(2):
+            api.i8_dense_gemm(a8, sa, w_d, sw_d, K, N, scale_mode=0)
+        order.append(["ti8_gemm_kernel<4, 0, 1, true>", f"dense {K}x{N}", K, N, 2 * 256 * K * N])
+        words = torch.randint(-2**31, 2**31 - 1, (K * N * KB // 32,), dtype=torch.int32, device=dev)
+        swc = api.trellis_i8_table(words, K, N, KB, True)
+        svh = torch.from_numpy(WL.svh_scales(N, 8)).to(dev)
+        for _ in range(2):
+            api.trellis_gemm_i8(a8, sa, words, swc, svh, K, N, KB, coarse=True, skg=1 if N > 8192 else 4)
+        order.append(["ti8_gemm_kernel<4, 0, 0, false>", f"trellis coarse {K}x{N}", K, N, 2 * 256 * K * N])
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_prefill": "done", "launches_each": 2, "order": order}), flush=True)
 
 
 def bench_m256(api, WL, KB, R=3):
