@@ -78,7 +78,12 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
     const unsigned own = (tile + KB * c) * 4u, hist = (tile + (KB * c - 1 + 8 * KB) % (8 * KB)) * 4u;
     constexpr int RA = MR / 4, AU = RA / 8;       // rows per producer; 16-byte loads per lane per step
     const r4_rsrc ar = mk_rsrc(A, (unsigned)((size_t)MR * K * 2));
-    const int ar0 = p * RA + (lane >> 3), ac = lane & 7;
+    // load u covers rows {a, a+1, a+2, a+3, a+8, .., a+11}, a = 4 (u & 1) + 16 (u >> 1), lane group i = lane >> 3
+    // taking row a + (i & 1) + 8 ((i >> 1) & 1) + 2 (i >> 2): each 32-lane half of a quad write then holds rows whose
+    // swizzles differ in bit 2 (two disjoint 64-byte chunk groups), so the writes are free of bank conflicts
+    const int li = lane >> 3, ac = lane & 7;
+    const int ar0 = p * RA + (li & 1) + 8 * ((li >> 1) & 1) + 2 * (li >> 2);
+    auto arow = [&](int u) { return ar0 + 4 * (u & 1) + 16 * (u >> 1); };
     const unsigned aoff = (unsigned)(((size_t)ar0 * K + (size_t)kt0 * 16 + ac * 8) * 2);
 
     struct St {
@@ -99,7 +104,7 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
 #pragma unroll
       for (int u = 0; u < AU; ++u)
         s.a[u] = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              ar, aoff + (unsigned)(u * 8 * K * 2) + (unsigned)sc * 128u, 0, 0));
+                                              ar, aoff + (unsigned)((arow(u) - ar0) * K * 2) + (unsigned)sc * 128u, 0, 0));
     };
     auto put = [&](const St& s, int st) {
       unsigned char* stg = lds + (st & 1) * kStage;
@@ -109,8 +114,8 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
 #pragma unroll
       for (int u = 0; u < AU; ++u) {
         unsigned char* row = stg + (ac & 1) * 8;
-        *(r4u2*)(row + m2_slot(ar0 + 8 * u, ac >> 1)) = (r4u2){s.a[u][0], s.a[u][1]};
-        *(r4u2*)(row + m2_slot(ar0 + 8 * u, 4 + (ac >> 1))) = (r4u2){s.a[u][2], s.a[u][3]};
+        *(r4u2*)(row + m2_slot(arow(u), ac >> 1)) = (r4u2){s.a[u][0], s.a[u][1]};
+        *(r4u2*)(row + m2_slot(arow(u), 4 + (ac >> 1))) = (r4u2){s.a[u][2], s.a[u][3]};
       }
       unsigned d[2][2][4];
       r4_decode<KB>(s.w, d);
