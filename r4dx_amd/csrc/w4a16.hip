@@ -12,13 +12,28 @@
 // low half, f16(-(1024 + zero)) in the high half.
 //
 // DESIGN (MI355X): HBM-bound. A wave streams two row tiles (32 output columns) over all of K, one
-// coalesced dwordx4 per lane per 64-k block: lane l takes tile 2p + ((l & 31) >> 4), lh = l >> 5,
-// r = l & 15 -- exactly the B operand of v_mfma_f32_32x32x16_f16 (lane = column l & 31, k-half l >> 5)
-// for each of its four dwords s. Dequant per dword: one xor (the ^ 8), four and_or into the f16 bits
-// of 1024 + q, four packed f16 adds of -(1024 + zero): element e of the fragment is nibble
-// {0, 4, 1, 5, 2, 6, 3, 7}[e]. A is staged once per workgroup in LDS in that element order. A group's
-// MFMA chain starts from zero and is added into the fp32 accumulator times the lane's column scale.
-// N = 248 320 gives 7 760 waves of work, so no split of K is needed.
+// coalesced dwordx4 per lane per 64-k block (lane l: tile 2p + ((l & 31) >> 4), lh = l >> 5, r = l & 15),
+// w4_pf blocks in flight in a statically indexed ring; the loads are nontemporal (each weight byte is
+// read once).
+//
+// Dequant per dword (8 nibbles, nibble i at k = 16 s + 4 lh + {0, 8, 1, 9, 2, 10, 3, 11}[i]): masks
+// 0x000F000F and 0x00F000F0 of the dword and of the dword >> 8 pick the nibble pairs (0, 4), (1, 5),
+// (2, 6), (3, 7); one and-xor each gives the f16 bits of 1024 + q (the ^ 8 folded into the xor constant)
+// for a low nibble and of 1024 + 16 q for a high one; one packed f16 add of -(1024 + z), resp.
+// -(1024 + 16 z), gives q - z, resp. 16 (q - z), exactly. Pairs (0, 4), (2, 6) are k +0, +2, +1, +3
+// ("U", unscaled) and (1, 5), (3, 7) are k +8, +10, +9, +11 ("S", scaled by 16). A 64-k block is four
+// MFMAs of eight elements per lane: U of dwords (0, 1), U of (2, 3), S of (0, 1), S of (2, 3) -- each
+// inside one group of 32. The two chains are combined as (U + S / 16) * scale: the 1 / 16 undoes the
+// factor 16 exactly (a power of two). The A fragment of an MFMA is two runs of four k in that order,
+// staged in LDS with one row of zeros per (block, MFMA, k-half) for the lanes whose row is absent.
+//
+// Two MFMA forms. M <= 8: v_mfma_f32_16x16x32_f16 with rows (2 m + tile): lane (n, kq) holds the B data
+// of tile kq & 1, k-half kq >> 1, and A row rho is nonzero only where rho & 1 == kq & 1, so output row
+// 2 m + t is row m of tile t -- one 16x16x32 covers both tiles at half the MFMA cycles of a 32x32x16.
+// M > 8: v_mfma_f32_32x32x16_f16 (lane = column l & 31, k-half l >> 5), MT row tiles of 32.
+//
+// A is staged per chunk of KC 64-k blocks (all of K when it fits the LDS budget); a chunk change is a
+// block barrier. N = 248 320 gives 7 760 waves of work, so no split of K is needed.
 #include "r4d_dev.h"
 #include "r4d_host.h"
 #include "r4d_mi355x.h"
@@ -29,147 +44,256 @@ typedef __amdgpu_buffer_rsrc_t r4_rsrc;
 __device__ __forceinline__ r4_rsrc mk_rsrc(const void* p, unsigned bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
 }
-__device__ __forceinline__ r4f16 mfma32(r4h8 a, r4h8 b, r4f16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+
+constexpr int kWaves = 8;          // 8 waves = 256 output columns per workgroup
+// weight steps in flight per wave: 6 in the 16x16x32 form at G = 64 (measured faster there), else 4
+__host__ __device__ constexpr int w4_pf(int G, bool small) { return G == 64 && small ? 6 : 4; }
+constexpr int kNT = 2;             // cache policy of the weight loads: nontemporal (read once, streamed)
+constexpr int kLdsBudget = 40 * 1024;   // A chunk bytes per workgroup (four workgroups per CU)
+
+// 64-k blocks per A chunk for M rows (M + 1 staged): a multiple of pf, at most KB64 rounded up to one.
+__host__ __device__ inline int w4_chunk(int M, int KB64, int pf) {
+  int kc = kLdsBudget / (128 * (M + 1));
+  kc -= kc % pf;
+  const int all = (KB64 + pf - 1) / pf * pf;
+  return kc < all ? kc : all;
 }
 
-// The k offset (inside a 16-k step, before the lane half's 4 lh) of fragment element e.
-__host__ __device__ constexpr int w4_elem_k(int e) {
-  // e -> nibble {0,4,1,5,2,6,3,7}[e] -> k {0,8,1,9,2,10,3,11}[nibble]
-  return e == 0 ? 0 : e == 1 ? 2 : e == 2 ? 8 : e == 3 ? 10 : e == 4 ? 1 : e == 5 ? 3 : e == 6 ? 9 : 11;
+// B operand of MFMA c (0: U of dwords 0,1; 1: U of 2,3; 2: S of 0,1; 3: S of 2,3) from the dequantized
+// halves: u[s] = (k +0,+2 ; +1,+3), v[s] = (k +8,+10 ; +9,+11).
+struct W4B {
+  r4u2 u[4], v[4];
+};
+__device__ __forceinline__ void w4_dequant(const r4u4 w, const unsigned (&nz)[4], const unsigned (&nz16)[4], W4B& o) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const unsigned x = w[s], y = x >> 8;
+    const unsigned p0 = (x & 0x000F000Fu) ^ 0x64086408u, p1 = (x & 0x00F000F0u) ^ 0x64806480u;
+    const unsigned p2 = (y & 0x000F000Fu) ^ 0x64086408u, p3 = (y & 0x00F000F0u) ^ 0x64806480u;
+    const r4h2 z = __builtin_bit_cast(r4h2, nz[s]), z16 = __builtin_bit_cast(r4h2, nz16[s]);
+    o.u[s][0] = __builtin_bit_cast(unsigned, __builtin_bit_cast(r4h2, p0) + z);
+    o.u[s][1] = __builtin_bit_cast(unsigned, __builtin_bit_cast(r4h2, p2) + z);
+    o.v[s][0] = __builtin_bit_cast(unsigned, __builtin_bit_cast(r4h2, p1) + z16);
+    o.v[s][1] = __builtin_bit_cast(unsigned, __builtin_bit_cast(r4h2, p3) + z16);
+  }
+}
+__device__ __forceinline__ r4h8 w4_bop(const W4B& b, int c) {
+  const r4u2 lo = c == 0 ? b.u[0] : c == 1 ? b.u[2] : c == 2 ? b.v[0] : b.v[2];
+  const r4u2 hi = c == 0 ? b.u[1] : c == 1 ? b.u[3] : c == 2 ? b.v[1] : b.v[3];
+  return __builtin_bit_cast(r4h8, (r4u4){lo[0], lo[1], hi[0], hi[1]});
+}
+// k offset (in the 64-k block, before 4 lh) of the first run of MFMA c's A fragment; the second run is +16
+__host__ __device__ constexpr int w4_run_k(int c) { return c == 0 ? 0 : c == 1 ? 32 : c == 2 ? 8 : 40; }
+
+// (f16 -(1024 + z), f16 -(1024 + 16 z)) pairs of one Wsz word: -(1024 + 16 z) = 16 (-(1024 + z)) + 15360,
+// exact in f16 (integers below 2048)
+__device__ __forceinline__ void w4_zeros(unsigned szw, unsigned& nz, unsigned& nz16) {
+  nz = __builtin_amdgcn_perm(szw, szw, 0x03020302u);
+  nz16 = __builtin_bit_cast(unsigned, __builtin_elementwise_fma(__builtin_bit_cast(r4h2, nz),
+                                                                (r4h2){(_Float16)16.0f, (_Float16)16.0f},
+                                                                (r4h2){(_Float16)15360.0f, (_Float16)15360.0f}));
 }
 
-constexpr int kWaves = 8;      // 8 waves = 256 output columns per workgroup
-constexpr int kPF = 6;         // weight steps in flight per wave
-
-// MT = row tiles of 32 (M <= 32: 1, M <= 64: 2). G = group (32 or 64). OUTF = fp32 output.
-template <int G, int MT, bool OUTF>
+// SMALL: the 16x16x32 form (M <= 8). MT: row tiles of 32 in the 32x32x16 form.
+template <int G, bool SMALL, int MT, bool OUTF>
 __global__ __launch_bounds__(64 * kWaves) void w4_kernel(const unsigned short* __restrict__ A,
                                                           const unsigned* __restrict__ Wq,
                                                           const unsigned* __restrict__ Wsz,
                                                           void* __restrict__ Cv, int M, int K, int N) {
-  extern __shared__ r4u4 alds[];             // [kb][s][lh][M][8 halves] + a zero block
+  extern __shared__ r4u4 alds[];   // chunk fragments [kb][c][lh][M] of 8 halves, then a zero block
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int KB64 = K >> 6, groups = K / G;
   const int tiles = N >> 4;
-  const int t0 = (blockIdx.x * kWaves + wave) * 2;     // this wave's first row tile
+  constexpr int kPF = w4_pf(G, SMALL);
+  const int KC = w4_chunk(M, KB64, kPF);
+  const int M1 = M + 1;                        // staged rows: row M is zero
+  int t0 = (blockIdx.x * kWaves + (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * 2;
+  const bool live = t0 < tiles;
+  if (!live) t0 = tiles - 1;                   // a spare wave streams the last tile and stores nothing
   const int tl = t0 + ((lane & 31) >> 4), lh = lane >> 5, r = lane & 15;
-  const size_t zero_blk = (size_t)KB64 * 4 * 2 * M;
 
-  // Stage A in the fragment element order: fragment (kb, s, lh, m) element e = A[m][64 kb + 16 s + 4 lh + w4_elem_k(e)].
-  for (int i = threadIdx.x; i < KB64 * 4 * 2 * M; i += 64 * kWaves) {
-    const int m = i % M, rest = i / M, h = rest & 1, ks = rest >> 1;   // ks = kb * 4 + s
-    const unsigned short* src = A + (size_t)m * K + 16 * ks + 4 * h;
-    const r4u2 lo = *(const r4u2*)src, hi = *(const r4u2*)(src + 8);   // k +0..3, +8..11
-    // elements: (k0, k2) (k8, k10) (k1, k3) (k9, k11)
-    r4u4 v;
-    v[0] = __builtin_amdgcn_perm(lo[1], lo[0], 0x05040100u);
-    v[1] = __builtin_amdgcn_perm(hi[1], hi[0], 0x05040100u);
-    v[2] = __builtin_amdgcn_perm(lo[1], lo[0], 0x07060302u);
-    v[3] = __builtin_amdgcn_perm(hi[1], hi[0], 0x07060302u);
-    alds[i] = v;
-  }
-  if (threadIdx.x == 0) alds[zero_blk] = (r4u4){0u, 0u, 0u, 0u};
-  __syncthreads();
-  if (t0 >= tiles) return;
-
-  // lane's weights: 16 bytes of block (tl, kb) at lh, r; the tile's blocks are consecutive in kb
   const r4_rsrc wr = mk_rsrc(Wq, (unsigned)((size_t)N * K / 2));
   const unsigned wlane = (unsigned)((((size_t)tl * KB64) * 2 + lh) * 16 + r) * 16u;
   const r4_rsrc sr = mk_rsrc(Wsz, (unsigned)((size_t)N * groups * 4));
-  const unsigned slane = (unsigned)(((size_t)tl * groups * 16) + r) * 4u;
+  // the lane's own tile (its zero point) and, in the SMALL form, both tiles' scales at column r
+  const unsigned sown = (unsigned)(((size_t)tl * groups * 16) + r) * 4u;
+  const unsigned st0 = (unsigned)(((size_t)t0 * groups * 16) + r) * 4u;
+  const unsigned st1 = (unsigned)(((size_t)(t0 + 1) * groups * 16) + r) * 4u;
+  constexpr int NG = 64 / G;                  // groups per 64-k block
+  constexpr int NS = SMALL ? 2 : 1;           // scale words per group
+  const bool own1 = ((lane >> 4) & 1) != 0;   // SMALL: the lane's own tile is t0 + 1
 
-  // A fragment address per row tile: (kb, s) advance; rows >= M read the zero block
-  unsigned a_lane[MT];
+  // A fragment byte offsets in the chunk (without the kb, c term) per row tile
+  constexpr int NA = SMALL ? 1 : MT;
+  unsigned a_lane[NA];
 #pragma unroll
-  for (int i = 0; i < MT; ++i) {
-    const int m = i * 32 + (lane & 31);
-    a_lane[i] = m < M ? (unsigned)((lh * M + m) * 16) : 0xFFFFFFFFu;
+  for (int i = 0; i < NA; ++i) {
+    int m, h;
+    bool ok;
+    if constexpr (SMALL) {
+      const int rho = lane & 15, kq = lane >> 4;
+      m = rho >> 1; h = kq >> 1; ok = (rho & 1) == (kq & 1) && m < M;
+    } else {
+      m = i * 32 + (lane & 31); h = lh; ok = m < M;
+    }
+    a_lane[i] = (unsigned)((h * M1 + (ok ? m : M)) * 16);
   }
-  auto afrag = [&](int i, int kb, int s) -> r4h8 {
-    const unsigned off = a_lane[i] != 0xFFFFFFFFu ? (unsigned)((kb * 4 + s) * 2 * M * 16) + a_lane[i]
-                                                  : (unsigned)(zero_blk * 16);
+  const unsigned kb_stride = 8u * (unsigned)M1 * 16u;   // bytes per 64-k block in the chunk
+  auto afrag = [&](int i, int kbl, int c) -> r4h8 {
+    const unsigned off = (unsigned)kbl * kb_stride + (unsigned)c * 2u * M1 * 16u + a_lane[i];
     return __builtin_bit_cast(r4h8, *(const r4u4*)((const char*)alds + off));
   };
+  // stage 64-k blocks [kb0, kb0 + KC) of A: fragment ((kbl * 4 + c) * 2 + h) * M1 + m holds
+  // A[m][64 kb + run_k(c) + 4 h + {0, 2, 1, 3, 16, 18, 17, 19}] (row M: zeros)
+  auto stage = [&](int kb0) {
+    const int n = min(KC, KB64 - kb0) * 8 * M1;
+    for (int i = threadIdx.x; i < n; i += 64 * kWaves) {
+      const int m = i % M1, rest = i / M1, h = rest & 1, c = (rest >> 1) & 3, kbl = rest >> 3;
+      r4u4 v = {0u, 0u, 0u, 0u};
+      if (m < M) {
+        const unsigned short* src = A + (size_t)m * K + 64 * (kb0 + kbl) + w4_run_k(c) + 4 * h;
+        const r4u2 lo = *(const r4u2*)src, hi = *(const r4u2*)(src + 16);
+        v[0] = __builtin_amdgcn_perm(lo[1], lo[0], 0x05040100u);
+        v[1] = __builtin_amdgcn_perm(lo[1], lo[0], 0x07060302u);
+        v[2] = __builtin_amdgcn_perm(hi[1], hi[0], 0x05040100u);
+        v[3] = __builtin_amdgcn_perm(hi[1], hi[0], 0x07060302u);
+      }
+      alds[i] = v;
+    }
+  };
 
-  r4f16 acc[MT];
+  using Acc = typename std::conditional<SMALL, r4f4, r4f16>::type;
+  Acc acc[NA];
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
+  for (int i = 0; i < NA; ++i) acc[i] = Acc{};
 
   struct St {
     r4u4 w;
-    unsigned sz[G == 32 ? 2 : 1];
+    unsigned sz[NG * NS];
   };
   auto load = [&](St& s, int kb) {
     const int kc = kb < KB64 ? kb : KB64 - 1;
-    s.w = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(wr, wlane + (unsigned)kc * 512u, 0, 0));
-    if constexpr (G == 64) {
-      s.sz[0] = __builtin_amdgcn_raw_buffer_load_b32(sr, slane + (unsigned)kc * 64u, 0, 0);
-    } else {
-      s.sz[0] = __builtin_amdgcn_raw_buffer_load_b32(sr, slane + (unsigned)(2 * kc) * 64u, 0, 0);
-      s.sz[1] = __builtin_amdgcn_raw_buffer_load_b32(sr, slane + (unsigned)(2 * kc + 1) * 64u, 0, 0);
+    s.w = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(wr, wlane + (unsigned)kc * 512u, 0, kNT));
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const unsigned go = (unsigned)(NG * kc + g) * 64u;
+      if constexpr (SMALL) {
+        s.sz[2 * g] = __builtin_amdgcn_raw_buffer_load_b32(sr, st0 + go, 0, kNT);
+        s.sz[2 * g + 1] = __builtin_amdgcn_raw_buffer_load_b32(sr, st1 + go, 0, kNT);
+      } else {
+        s.sz[g] = __builtin_amdgcn_raw_buffer_load_b32(sr, sown + go, 0, kNT);
+      }
     }
   };
-  auto compute = [&](const St& s, int kb) {
-    // dequant the four dwords: (q - zero) as f16 pairs in fragment order
-    r4h8 b[4];
+  auto compute = [&](const St& s, int kbl) {
+    unsigned nz[4], nz16[4];
 #pragma unroll
-    for (int sI = 0; sI < 4; ++sI) {
-      const unsigned nzw = s.sz[G == 32 ? (sI >> 1) : 0] >> 16;
-      const r4h2 nz = __builtin_bit_cast(r4h2, nzw | (nzw << 16));
-      const unsigned x = s.w[sI] ^ 0x88888888u;
-      r4u4 f;
+    for (int g = 0; g < NG; ++g) {
+      const unsigned own = SMALL ? (own1 ? s.sz[2 * g + 1] : s.sz[2 * g]) : s.sz[g];
+      unsigned a, b;
+      w4_zeros(own, a, b);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const unsigned p = ((x >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
-        f[j] = __builtin_bit_cast(unsigned, __builtin_bit_cast(r4h2, p) + nz);
-      }
-      b[sI] = __builtin_bit_cast(r4h8, f);
+      for (int q = 0; q < 4 / NG; ++q) { nz[g * (4 / NG) + q] = a; nz16[g * (4 / NG) + q] = b; }
     }
+    W4B bq;
+    w4_dequant(s.w, nz, nz16, bq);
 #pragma unroll
-    for (int gi = 0; gi < (G == 32 ? 2 : 1); ++gi) {
-      const float sc = r4_f16_to_f32((unsigned short)(s.sz[gi] & 0xFFFFu));
+    for (int g = 0; g < NG; ++g) {
+      // group g: G = 64 -> U chain (c 0, 1), S chain (c 2, 3); G = 32 -> g 0: c 0 / 2, g 1: c 1 / 3
 #pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        r4f16 tmp;
+      for (int i = 0; i < NA; ++i) {
+        Acc tu, ts;
+        if constexpr (SMALL) {
+          tu = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag(i, kbl, G == 64 ? 0 : g), w4_bop(bq, G == 64 ? 0 : g), Acc{}, 0, 0, 0);
+          ts = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag(i, kbl, G == 64 ? 2 : 2 + g), w4_bop(bq, G == 64 ? 2 : 2 + g), Acc{}, 0, 0, 0);
+          if constexpr (G == 64) {
+            tu = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag(i, kbl, 1), w4_bop(bq, 1), tu, 0, 0, 0);
+            ts = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag(i, kbl, 3), w4_bop(bq, 3), ts, 0, 0, 0);
+          }
+          // output rows 4 (lane >> 4) + e = 2 m + t: tile t = e & 1 (rows m >= M have zero A and stay 0)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) tmp[e] = 0.f;
+          for (int e = 0; e < 4; ++e) {
+            const float sc = r4_f16_to_f32((unsigned short)(s.sz[2 * g + (e & 1)] & 0xFFFFu));
+            acc[i][e] = __builtin_fmaf(__builtin_fmaf(ts[e], 0.0625f, tu[e]), sc, acc[i][e]);
+          }
+        } else {
+          tu = __builtin_amdgcn_mfma_f32_32x32x16_f16(afrag(i, kbl, G == 64 ? 0 : g), w4_bop(bq, G == 64 ? 0 : g), Acc{}, 0, 0, 0);
+          ts = __builtin_amdgcn_mfma_f32_32x32x16_f16(afrag(i, kbl, G == 64 ? 2 : 2 + g), w4_bop(bq, G == 64 ? 2 : 2 + g), Acc{}, 0, 0, 0);
+          if constexpr (G == 64) {
+            tu = __builtin_amdgcn_mfma_f32_32x32x16_f16(afrag(i, kbl, 1), w4_bop(bq, 1), tu, 0, 0, 0);
+            ts = __builtin_amdgcn_mfma_f32_32x32x16_f16(afrag(i, kbl, 3), w4_bop(bq, 3), ts, 0, 0, 0);
+          }
+          const float sc = r4_f16_to_f32((unsigned short)(s.sz[g] & 0xFFFFu));
+          // only the rows this launch has: row = (e / 4) * 8 + lh * 4 + e % 4
 #pragma unroll
-        for (int sI = gi * (G / 16); sI < (gi + 1) * (G / 16); ++sI) tmp = mfma32(afrag(i, kb, sI), b[sI], tmp);
-        // only the rows this launch has: row = (e / 4) * 8 + lh * 4 + e % 4
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if (i * 32 + (e >> 2) * 8 < M) acc[i][e] = __builtin_fmaf(tmp[e], sc, acc[i][e]);
+          for (int e = 0; e < 16; ++e)
+            if (i * 32 + (e >> 2) * 8 < M) acc[i][e] = __builtin_fmaf(__builtin_fmaf(ts[e], 0.0625f, tu[e]), sc, acc[i][e]);
+        }
       }
     }
   };
 
+  // The ring is indexed statically (the loop unrolled by kPF): a register copy of a slot whose load is
+  // still in flight would wait for it and leave one load in flight. Chunk boundaries fall on multiples
+  // of kPF (KC is one).
   St ring[kPF];
 #pragma unroll
   for (int i = 0; i < kPF; ++i) load(ring[i], i);
-  for (int kb = 0; kb < KB64; ++kb) {
-    compute(ring[0], kb);
+  const int full = KB64 - KB64 % kPF;
+  int kb_chunk = 0;
+  stage(0);
+  __syncthreads();
+  for (int kb = 0; kb < full; kb += kPF) {
+    if (kb - kb_chunk == KC) {
+      __syncthreads();
+      kb_chunk = kb;
+      stage(kb);
+      __syncthreads();
+    }
 #pragma unroll
-    for (int i = 0; i + 1 < kPF; ++i) ring[i] = ring[i + 1];
-    load(ring[kPF - 1], kb + kPF);
+    for (int i = 0; i < kPF; ++i) {
+      compute(ring[i], kb - kb_chunk + i);
+      load(ring[i], kb + i + kPF);
+    }
   }
+  if (full < KB64) {
+    if (full - kb_chunk == KC) {
+      __syncthreads();
+      kb_chunk = full;
+      stage(full);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < kPF; ++i)
+      if (full + i < KB64) compute(ring[i], full - kb_chunk + i);
+  }
+  if (!live) return;
 
-  // lane holds column n = 16 t0 + (lane & 31), rows (e / 4) * 8 + lh * 4 + e % 4 of each row tile
-  const int n = 16 * t0 + (lane & 31);
-  if (n >= N) return;
+  if constexpr (SMALL) {
+    // lane: column 16 t + (lane & 15), rows 4 (lane >> 4) + e = 2 m + t
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int m = i * 32 + (e >> 2) * 8 + lh * 4 + (e & 3);
-      if (m < M) {
-        if constexpr (OUTF) ((float*)Cv)[(size_t)m * N + n] = acc[i][e];
-        else ((unsigned short*)Cv)[(size_t)m * N + n] = r4_bf16_rn(acc[i][e]);
+    for (int e = 0; e < 4; ++e) {
+      const int m = 2 * (lane >> 4) + (e >> 1), n = 16 * (t0 + (e & 1)) + (lane & 15);
+      if (m < M && n < N) {
+        if constexpr (OUTF) ((float*)Cv)[(size_t)m * N + n] = acc[0][e];
+        else ((unsigned short*)Cv)[(size_t)m * N + n] = r4_bf16_rn(acc[0][e]);
       }
     }
+  } else {
+    // lane holds column n = 16 t0 + (lane & 31), rows (e / 4) * 8 + lh * 4 + e % 4 of each row tile
+    const int n = 16 * t0 + (lane & 31);
+    if (n >= N) return;
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = i * 32 + (e >> 2) * 8 + lh * 4 + (e & 3);
+        if (m < M) {
+          if constexpr (OUTF) ((float*)Cv)[(size_t)m * N + n] = acc[i][e];
+          else ((unsigned short*)Cv)[(size_t)m * N + n] = r4_bf16_rn(acc[i][e]);
+        }
+      }
+  }
 }
 
 std::string w4_check(int group, int M, int K, int N) {
@@ -177,7 +301,8 @@ std::string w4_check(int group, int M, int K, int N) {
   if (M < 1 || M > 64) return "M must be 1..64";
   if (N <= 0 || N % 16) return "N must be a positive multiple of 16";
   if (K <= 0 || K % 64) return "K must be a positive multiple of 64 (the packed 64-k block)";
-  if ((size_t)(K / 64) * 8 * M * 16 + 16 > 144 * 1024) return "M x K too large for the LDS copy of A";
+  if ((size_t)N * K / 2 >= (1ull << 32) || (size_t)N * (K / group) * 4 >= (1ull << 32))
+    return "N x K too large for 32-bit buffer offsets (4 GiB of packed weights)";
   return "";
 }
 
@@ -186,12 +311,13 @@ void w4_launch(int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int 
   const int tiles = N / 16;
   const int waves = (tiles + 1) / 2;
   dim3 grid((waves + kWaves - 1) / kWaves), block(64 * kWaves);
-  const size_t smem = (size_t)(K / 64) * 8 * M * 16 + 16;
+  const size_t smem = (size_t)w4_chunk(M, K / 64, w4_pf(G, M <= 8)) * 8 * (M + 1) * 16;
   auto Ap = (const unsigned short*)a;
   auto Wp = (const unsigned*)wq;
   auto Sp = (const unsigned*)wsz;
-  if (M <= 32) hipLaunchKernelGGL((w4_kernel<G, 1, OUTF>), grid, block, smem, st, Ap, Wp, Sp, (void*)c, M, K, N);
-  else hipLaunchKernelGGL((w4_kernel<G, 2, OUTF>), grid, block, smem, st, Ap, Wp, Sp, (void*)c, M, K, N);
+  if (M <= 8) hipLaunchKernelGGL((w4_kernel<G, true, 1, OUTF>), grid, block, smem, st, Ap, Wp, Sp, (void*)c, M, K, N);
+  else if (M <= 32) hipLaunchKernelGGL((w4_kernel<G, false, 1, OUTF>), grid, block, smem, st, Ap, Wp, Sp, (void*)c, M, K, N);
+  else hipLaunchKernelGGL((w4_kernel<G, false, 2, OUTF>), grid, block, smem, st, Ap, Wp, Sp, (void*)c, M, K, N);
 }
 
 void w4_run(int group, int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int N, bool outf,

@@ -64,5 +64,6 @@ def test_w4a16_checks(L):
     assert b"group" in ck(128, 1, 5120, 248320)
     assert b"N must" in ck(64, 1, 5120, 248321)
     assert b"K must" in ck(64, 1, 5100, 256)
+    assert ck(64, 64, 5120, 248320) is None            # A is staged in K chunks: any M up to 64
     assert [L.r4d_gemm_w4a16_nt_m64_has_group(g) for g in (16, 32, 64, 128)] == [0, 1, 1, 0]
     assert L.r4d_gemm_w4a16_nt_m64_group() == 64 and L.r4d_gemm_w4a16_nt_m64_max_m() == 64

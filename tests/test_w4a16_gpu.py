@@ -75,6 +75,21 @@ def test_w4a16_random(group, M):
 
 
 @pytest.mark.parametrize("group", [32, 64])
+@pytest.mark.parametrize("M,N,K", [(1, 16, 448), (5, 48, 320), (8, 512, 5120), (9, 80, 704), (33, 256, 5120),
+                                   (64, 512, 5120), (64, 32, 8192)])
+def test_w4a16_shapes(group, M, N, K):
+    """Ragged shapes: one tile (spare waves), an odd tile count, K not a multiple of the prefetch depth,
+    A staged in several LDS chunks (M = 8 and 64 at K = 5120 and 8192), both MFMA forms and both row-tile
+    counts."""
+    banner("w4a16 shape", group, M, N, K)
+    wq, wsz = WL.w4a16_packed(N, K, group, 11 + M)
+    a = WL.activations_f16(M, K, 12).view(np.uint16)
+    c32 = api.w4a16_gemm(dev(a), dev(wq), dev(wsz), K, N, group, f32=True)
+    torch.cuda.synchronize()
+    assert close_rel(c32.cpu().numpy(), _ref(a, wq, wsz, N, K, group), 1e-3, 1e-4) <= 1.0
+
+
+@pytest.mark.parametrize("group", [32, 64])
 def test_config3_lm_head(group):
     """Full vocab: logits on a random subset of 4096 columns vs the fp64 oracle, argmax bit-exact vs the
     oracle's order over the kernel's logits."""
