@@ -95,6 +95,16 @@ __device__ __forceinline__ unsigned r4_window(const unsigned* W) {
   else return __builtin_amdgcn_alignbit(W[i], W[i + 1], 32 - off);
 }
 
+// The history word of a decode lane: the word before its own KB words in its tile's ring of 8 KB words
+// (lane c of an 8-lane group owns words KB c .. KB c + KB - 1) is the last own word of lane c - 1 mod 8
+// of the same group. Two DPP moves inside the 16-lane row (row_shr:1 gives lane i the value of lane
+// i - 1, row_shl:7 that of lane i + 7) and a select for c = 0 replace a second load per step.
+__device__ __forceinline__ unsigned r4_hist_word(unsigned last, int lane) {
+  const unsigned from_prev = (unsigned)__builtin_amdgcn_mov_dpp((int)last, 0x111, 0xF, 0xF, true);
+  const unsigned from_wrap = (unsigned)__builtin_amdgcn_mov_dpp((int)last, 0x107, 0xF, 0xF, true);
+  return (lane & 7) == 0 ? from_wrap : from_prev;
+}
+
 // Fragment element of position (m, j) of column slot cs = j >> 2: half h = m >> 1,
 // e = 4 ((j >> 1) & 1) + 2 (m & 1) + (j & 1)  (k = 2m + (j & 1) + 8 ((j >> 1) & 1)).
 // The decode writes each fragment as 4 dwords d[cs][h][e >> 1] (two elements per dword).

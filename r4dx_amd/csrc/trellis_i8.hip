@@ -69,14 +69,13 @@ __device__ __forceinline__ float ti8_amax16(const unsigned (&d)[2][2][4], int cs
 template <int KB>
 struct TileWords {
   r4_rsrc r;
-  unsigned own, hist;
+  unsigned own;   // the history word comes from lane c - 1 (r4_hist_word)
   __device__ __forceinline__ TileWords(const unsigned* W, int pair, int KT, int kt0, int ktw, int lane) {
     constexpr int BLK = 16 * KB;
     r = mk_rsrc(W + ((size_t)pair * KT + kt0) * BLK, (unsigned)ktw * BLK * 4u);
     const int q = lane >> 4, t = (lane >> 3) & 1, c = lane & 7;
     const unsigned tile = (unsigned)(q * 16 * KB + t * 8 * KB);
     own = (tile + KB * c) * 4u;
-    hist = (tile + (KB * c - 1 + 8 * KB) % (8 * KB)) * 4u;
   }
   __device__ __forceinline__ void load(unsigned (&w)[KB + 1], int st) const {
     const unsigned so = (unsigned)st * (4u * 16u * KB * 4u);
@@ -87,7 +86,6 @@ struct TileWords {
 #pragma unroll
       for (int i = 0; i < KB; ++i) w[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(r, own + so + 4 * i, 0, 0);
     }
-    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, hist + so, 0, 0);
   }
 };
 
@@ -103,6 +101,7 @@ __global__ __launch_bounds__(64) void ti8_wscale_kernel(const unsigned* __restri
   for (int st = 0; st < ktw / 4; ++st) {
     unsigned w[KB + 1], d[2][2][4];
     tw.load(w, st);
+    w[0] = r4_hist_word(w[KB], lane);
     r4_decode<KB>(w, d);
     m[0] = __builtin_fmaxf(m[0], ti8_amax16(d, 0));
     m[1] = __builtin_fmaxf(m[1], ti8_amax16(d, 1));
@@ -133,6 +132,7 @@ __global__ __launch_bounds__(64) void ti8_dump_kernel(const unsigned* __restrict
   const TileWords<KB> tw(W, pair, KT, 0, KT, lane);
   unsigned w[KB + 1], d[2][2][4];
   tw.load(w, st);
+  w[0] = r4_hist_word(w[KB], lane);
   r4_decode<KB>(w, d);
   const int q = lane >> 4, t = (lane >> 3) & 1, c = lane & 7;
   const int kt = 4 * st + q, kb = kt >> 3;
@@ -227,8 +227,11 @@ __device__ __forceinline__ void ti8_piece(const TI8Args& p, unsigned char (*bst)
       *(r4u2*)&bst[st & 1][wkt][ti8_bslot(nl)][8 * h] = (r4u2){wb[0], wb[1]};
       *(r4u2*)&bst[st & 1][wkt][ti8_bslot(nl + 8)][8 * h] = (r4u2){wb[2], wb[3]};
     } else {
-      unsigned d[2][2][4];
-      r4_decode<KB>(w, d);
+      unsigned d[2][2][4], wl[KB + 1];
+      wl[0] = r4_hist_word(w[KB], lane);
+#pragma unroll
+      for (int i = 1; i <= KB; ++i) wl[i] = w[i];
+      r4_decode<KB>(wl, d);
 #pragma unroll
       for (int cs = 0; cs < 2; ++cs) {
         const int nl = 32 * (wave & 3) + 16 * dt + 8 * cs + dc;
