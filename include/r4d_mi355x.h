@@ -30,7 +30,9 @@ extern "C" {
 void r4d_gemm_trellis_nt_m64(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
                              int64_t ws, int64_t tickets, int M, int K, int N, int KB, int WV, int SK,
                              int MT, int NP, int SKG, int U, int NT, float out_scale, int64_t stream);
-/* r4d.h:380-383 _raw: fp32 C [M][N] = A @ Q, no output transform (clk accepted, unused). */
+/* r4d.h:376-383 _raw: fp32 C [M][N] = A @ Q, no output transform; clk (0 = off): 4 uint64 that workgroup
+   (0, 0)'s thread 0 fills with the shader clock and the 100 MHz wall clock at entry and at the end of its own
+   work. */
 void r4d_gemm_trellis_nt_m64_raw(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t c, int64_t ws,
                                  int64_t tickets, int M, int K, int N, int KB, int WV, int SK, int MT,
                                  int NP, int SKG, int U, int NT, int64_t clk, int64_t stream);

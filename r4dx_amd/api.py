@@ -30,9 +30,11 @@ def trellis_gemv_skg(K, N, KB):
 
 
 def trellis_gemm_m64(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out=None, ws=None,
-                     tickets=None, out_scale=1.0, raw=False, stream=None, sk=0):
+                     tickets=None, out_scale=1.0, raw=False, stream=None, sk=0, clk=None):
     """C = r4d_gemm_trellis_nt_m64 (bf16 [M][N]) or, raw=True, its _raw fp32 A @ Q. sk = 1: the one-wave-per-
-    pair summation order that r4d_gemm_trellis_nt_m256 reproduces bit for bit."""
+    pair summation order that r4d_gemm_trellis_nt_m256 reproduces bit for bit. clk (raw only): an int64
+    device tensor of 4 that receives workgroup (0, 0)'s shader clock and wall clock at entry and at the end
+    of its own work."""
     L = lib()
     M = a0.shape[0]
     skg = trellis_gemv_skg(K, N, KB) if skg is None else skg
@@ -51,7 +53,7 @@ def trellis_gemm_m64(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out=
     st = _stream(stream)
     if raw:
         L.r4d_gemm_trellis_nt_m64_raw(_p(a0), _p(a1), n_split, _p(w), _p(out), _p(ws), _p(tickets),
-                                      M, K, N, KB, 0, sk, 0, 0, skg, 0, 0, 0, st)
+                                      M, K, N, KB, 0, sk, 0, 0, skg, 0, 0, _p(clk), st)
     else:
         L.r4d_gemm_trellis_nt_m64(_p(a0), _p(a1), n_split, _p(w), _p(svh), _p(out), _p(ws), _p(tickets),
                                   M, K, N, KB, 0, sk, 0, 0, skg, 0, 0, float(out_scale), st)

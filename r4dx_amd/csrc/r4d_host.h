@@ -60,4 +60,7 @@ struct r4d_gemv_args {
   // SK = 1: one wave per tile pair over the whole K slice (the workgroup holds a 128-column group) also
   // when the launch is split -- the summation order r4d_gemm_trellis_nt_m256 reproduces
   int sk1;
+  // the _raw entry's clock probe: 4 uint64 (shader clock, wall clock at entry; the same at the end of
+  // workgroup (0, 0)'s own work), or 0
+  int64_t clk;
 };

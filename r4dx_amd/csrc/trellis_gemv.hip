@@ -97,7 +97,8 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     const unsigned short* __restrict__ A0, const unsigned short* __restrict__ A1, int n_split,
     const unsigned* __restrict__ W, const float* __restrict__ svh, void* __restrict__ Cv,
     float* __restrict__ ws, unsigned* __restrict__ tickets, int M, int K, int N, int SKG, int full,
-    float out_scale, const float* __restrict__ suh0, const float* __restrict__ suh1, float xscale) {
+    float out_scale, const float* __restrict__ suh0, const float* __restrict__ suh1, float xscale,
+    unsigned long long* __restrict__ clk) {
   constexpr int PF = 4;
   constexpr int NT = 64 * NPW * SK;
   constexpr int NW = NPW * SK;                 // waves
@@ -105,6 +106,13 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
   extern __shared__ r4u4 lds_raw[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // the _raw entry's clock probe (r4d.h:376-383): workgroup (0, 0)'s thread 0 records the shader clock and
+  // the 100 MHz wall clock at entry and at the end of its own work (its sums combined, before any output)
+  const bool probe = clk != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0;
+  if (probe) {
+    clk[0] = __builtin_amdgcn_s_memtime();
+    clk[1] = __builtin_amdgcn_s_memrealtime();
+  }
   const int pl = wave % NPW, ks = wave / NPW;
   const int ky = blockIdx.y;
   const int pair = blockIdx.x * NPW + pl;
@@ -307,6 +315,11 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     }
   }
 
+  if (probe) {
+    clk[2] = __builtin_amdgcn_s_memtime();
+    clk[3] = __builtin_amdgcn_s_memrealtime();
+  }
+
   // Lane l of wave (pl, ks = 0) holds rows 16 i + 4 (l >> 4) + j of column slot nb = l & 15 of
   // fragment cs: true column 32 pair + 16 (nb >> 3) + (nb & 7) + 8 cs.
   const int nb = lane & 15, rq = lane >> 4;
@@ -476,7 +489,7 @@ void launch_gemv(const r4d_gemv_args& a) {
                      (const unsigned short*)a.a0, (const unsigned short*)(a.a1 ? a.a1 : a.a0), a.n_split,
                      (const unsigned*)a.w, (const float*)a.svh, (void*)a.c, (float*)a.ws,
                      (unsigned*)a.tickets, a.M, a.K, a.N, a.SKG, a.full, a.out_scale, (const float*)a.suh0,
-                     (const float*)(a.suh1 ? a.suh1 : a.suh0), a.xscale);
+                     (const float*)(a.suh1 ? a.suh1 : a.suh0), a.xscale, (unsigned long long*)a.clk);
 }
 
 template <int KB, int MT, int NPW, int SK>
@@ -555,9 +568,10 @@ void r4d_gemm_trellis_nt_m64(int64_t a0, int64_t a1, int n_split, int64_t w, int
 void r4d_gemm_trellis_nt_m64_raw(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t c, int64_t ws,
                                  int64_t tickets, int M, int K, int N, int KB, int WV, int SK, int MT,
                                  int NP, int SKG, int U, int NT, int64_t clk, int64_t stream) {
-  (void)WV; (void)MT; (void)NP; (void)U; (void)NT; (void)clk;
+  (void)WV; (void)MT; (void)NP; (void)U; (void)NT;
   r4d_gemv_args a{a0, a1, n_split, w, 0, c, ws, tickets, M, K, N, KB, SKG, 0, 1.f, stream};
   a.sk1 = SK == 1;
+  a.clk = clk;
   tq_run(a, "gemm_trellis_nt_m64_raw");
 }
 

@@ -119,6 +119,24 @@ def test_one_hot_rows_return_q():
         assert np.array_equal(got[m], O.f16_bits_to_f32(q[k]))
 
 
+def test_raw_clock_probe():
+    """The _raw entry's clk (third_party/libr4d/r4d.h:376-383): workgroup (0, 0)'s thread 0 writes the shader
+    clock and the wall clock at entry and at the end of its own work; clk = 0 leaves the launch as it was."""
+    banner("clk")
+    K, N, KB = 5120, 6144, 4
+    words = _grid(K, N, KB, 9)
+    a = dev(WL.activations_f16(1, K, 10).view(np.uint16))
+    clk = torch.zeros(4, dtype=torch.int64, device="cuda")
+    raw = api.trellis_gemm_m64(a, dev(words), None, K, N, KB, skg=4, raw=True, clk=clk)
+    ref = api.trellis_gemm_m64(a, dev(words), None, K, N, KB, skg=4, raw=True)
+    torch.cuda.synchronize()
+    c = [int(v) for v in clk.cpu()]
+    assert c[2] > c[0] > 0 and c[3] > c[1] > 0, c
+    ghz = (c[2] - c[0]) / (c[3] - c[1]) * 0.1          # wall clock: 100 MHz
+    assert 0.3 < ghz < 4.0, ghz
+    assert torch.equal(raw, ref)
+
+
 def test_row_identity_and_determinism():
     """For M <= 16 a row's bits do not depend on M or on the other rows (the reference's row identity
     rule, src/model/linear.cpp:33-53, third_party/libr4d/r4d.h:370-371), and repeated launches are
