@@ -96,7 +96,7 @@ void r4d_gemm_w4a16_nt_m64_g(int group, int64_t a, int64_t wq, int64_t wsz, int6
                              int SK, int MB, int NPW, int NT, int64_t stream);
 /* No reference counterpart: the legality rules of the two entries above without launching. */
 const char* r4d_gemm_w4a16_nt_m64_check(int group, int M, int K, int N);
-/* No reference counterpart (BASELINE config 3 asks for fp32 logits; the reference C is bf16): the
+/* No reference counterpart (fp32 logits for the LM head's argmax; the reference C is bf16): the
  * same GEMM with fp32 C [M][N]. */
 void r4d_gemm_w4a16_nt_m64_f32(int group, int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int N,
                                int64_t stream);
@@ -185,7 +185,7 @@ void r4d_gemm_trellis_nt_i8c(int64_t a8_0, int64_t sa_0, int64_t a8_1, int64_t s
  * pointers. */
 void r4dx_trellis_input_bf16(int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh,
                              const int64_t* out, int prescale_log2, int64_t stream);
-/* The same for an f16 x (BASELINE's fp16 activations); no reference counterpart, same contract. */
+/* The same for an f16 x (fp16 activations); no reference counterpart, same contract. */
 void r4dx_trellis_input_f16(int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh,
                             const int64_t* out, int prescale_log2, int64_t stream);
 /* kernels.h:192-197 r4dx_fwht128_f32: in-place unnormalised FWHT of each 128-float block (use_lds

@@ -1,4 +1,4 @@
-"""Synthetic inputs of BASELINE.json's configs (numpy, seeded).  No network, no checkpoints: the
+"""Synthetic inputs of the benchmark workloads (numpy, seeded).  No network, no checkpoints: the
 trellis words are uniform random uint32 (every 32-bit word is a valid ring), the Hadamard signs are
 random +-1, and the channel scales are log-normal, exactly as the configs describe."""
 import numpy as np
@@ -62,7 +62,7 @@ def trellis_linear(K, N, KB, seed):
 
 
 def w4a16_packed(N, K, group, seed):
-    """BASELINE config 3's weights directly in the packed form: uniform random nibbles, per (row, group)
+    """The LM-head workload's (w4a16) weights directly in the packed form: uniform random nibbles, per (row, group)
     an fp16 scale ~ lognormal around 0.02 and an int4 zero point uniform in 0..15.
     Returns (wq uint32 [N*K/8], wsz uint32 [N/16][K/group][16])."""
     rng = np.random.default_rng(seed)
@@ -76,7 +76,7 @@ def w4a16_packed(N, K, group, seed):
 
 
 def int8_case(K, N, seed, M=256):
-    """activations f16 Student-t (nu = 4); weights int8 uniform in [-127, 127] with an
+    """The int8 prefill workload: activations f16 Student-t (nu = 4); weights int8 uniform in [-127, 127] with an
     fp32 scale per output column (log-normal around 0.01)."""
     rng = np.random.default_rng(seed)
     x = rng.standard_t(4, (M, K)).astype(np.float16)

@@ -1,5 +1,5 @@
 """GPU parity of the int8 path (activation quantizers, the dense int8 x int8 GEMM) through the C ABI.
-M = 256, (K, N) = (5120, 17408) and (17408, 5120), Student-t activations.
+The int8 prefill workload (config 4): M = 256, (K, N) = (5120, 17408) and (17408, 5120), Student-t activations.
 
 Bars: quantized bytes and scales bit-exact; int32 accumulators exact; f16 outputs within 1e-3 relative
 error with a 1e-4 * rms(row) floor of the oracle's fp64 RefGemmInt8 (int8_gemm_proto_ref.h:95-110)."""

@@ -1,5 +1,5 @@
 """GPU parity of the M = 256 / 128 prefill trellis GEMM (r4d_gemm_trellis_nt_m256 and its _raw entry)
-through the C ABI.  A f16 ~N(0,1) with 1% of columns x20 (outlier channels).
+through the C ABI.  Workload (config 2): A f16 ~N(0,1) with 1% of columns x20 (outlier channels).
 
 Bars: fp32 sums within 1e-3 relative error with a 1e-4 * rms(row) floor of the fp64 matmul over the
 oracle-decoded weights; the bf16 linear bit-exact against the oracle's epilogue applied to the
@@ -110,7 +110,7 @@ def test_m256_rows_independent():
 
 @pytest.mark.parametrize("name,K,N", WL.LAYER_SHAPES)
 def test_config2_shapes(name, K, N):
-    """every projection at M = 256, KB 4 (and KB 5 on the MLP), against the fp64
+    """Config 2: every projection at M = 256, KB 4 (and KB 5 on the MLP), against the fp64
     matmul over the oracle-decoded weights."""
     for KB in ((4, 5) if name.startswith("mlp") else (4,)):
         banner("config2", name, K, N, KB)

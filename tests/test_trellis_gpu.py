@@ -169,7 +169,7 @@ def test_two_part_split():
 
 @pytest.mark.parametrize("name,K,N", WL.LAYER_SHAPES)
 def test_config1_shapes_m1_m8(name, K, N):
-    """every projection of the 27B-class layer at KB 4 and 5, M 1 and 8."""
+    """Config 1: every projection of the 27B-class layer at KB 4 and 5, M 1 and 8."""
     for KB in (4, 5):
         banner("config1", name, K, N, KB)
         words, svh, a, _, _ = _linear_case(K, N, KB, 8, hash(name) % 1000)

@@ -1,5 +1,5 @@
 """GPU parity of the w4a16 group-quantized GEMM (r4d_gemm_w4a16_nt_m64, _g, _f32) and the argmax entries
-through the C ABI, against the CPU oracle.  N = 248 320 (vocab), K = 5120, groups of
+through the C ABI, against the CPU oracle.  The LM-head workload (config 3): N = 248 320 (vocab), K = 5120, groups of
 32 and 64, M in {1, 8}.
 
 Bars: fp32 logits within 1e-3 relative error with a 1e-4 * rms(row) floor of the oracle's fp64
