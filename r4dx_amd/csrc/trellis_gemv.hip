@@ -48,7 +48,7 @@ struct LaneWords {
 constexpr int kWeightPolicy = 2;
 
 // One step's words of this lane from the slice buffer at step byte offset so (out of range -> 0).
-template <int KB>
+template <int KB, bool HIST = true>
 __device__ __forceinline__ void load_words(Words<KB>& s, r4_rsrc r, const LaneWords<KB>& lw, unsigned so) {
   if constexpr (KB == 4) {
     const r4u4 v = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(r, lw.own + so, 0, kWeightPolicy));
@@ -57,7 +57,7 @@ __device__ __forceinline__ void load_words(Words<KB>& s, r4_rsrc r, const LaneWo
 #pragma unroll
     for (int i = 0; i < KB; ++i) s.w[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(r, lw.own + so + 4 * i, 0, kWeightPolicy);
   }
-  s.w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, lw.hist + so, 0, kWeightPolicy);
+  if constexpr (HIST) s.w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, lw.hist + so, 0, kWeightPolicy);
 }
 
 // A row's two fragments (h = 0, 1) of one k-tile from the row buffer at byte offset off:
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
   // line instead of another wave's weights).
   auto load = [&](St& s, int sidx) {
     const int sc = min(sidx, nst - 1);
-    load_words<KB>(s.w, wr, lw, (unsigned)(st_beg + sc) * kStepBytes);
+    load_words<KB, XF == 0>(s.w, wr, lw, (unsigned)(st_beg + sc) * kStepBytes);
     if constexpr (!ALDS) {
       const bool ok = (st_beg + sc) * 4 + q < ktw;
 #pragma unroll
@@ -189,7 +189,17 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
       }
     }
     unsigned d[2][2][4];
-    r4_decode<KB>(s.w.w, d);
+    if constexpr (XF == 0) {
+      r4_decode<KB>(s.w.w, d);
+    } else {
+      // the fused-transform form takes the history word from lane c - 1 through the LDS crossbar (ds_bpermute,
+      // no VALU): measured 3 % faster there, while in the plain form the load is faster
+      unsigned wl[KB + 1];
+      wl[0] = (unsigned)__builtin_amdgcn_ds_bpermute(((lane & ~7) | ((lane + 7) & 7)) << 2, (int)s.w.w[KB]);
+#pragma unroll
+      for (int i = 1; i <= KB; ++i) wl[i] = s.w.w[i];
+      r4_decode<KB>(wl, d);
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const r4h8 b0 = r4_frag(d[0][h]), b1 = r4_frag(d[1][h]);
