@@ -188,6 +188,33 @@ void r4dx_trellis_input_bf16(int64_t x, int64_t M, int64_t K, int nout, const in
 /* The same for an f16 x (fp16 activations); no reference counterpart, same contract. */
 void r4dx_trellis_input_f16(int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh,
                             const int64_t* out, int prescale_log2, int64_t stream);
+/* kernels.h:130-147 the fused producers: r4dx_trellis_input_bf16 (nout = 1) over the bf16 value a producer kernel
+ * would have stored -- r4dx_silu_mul_trellis_bf16: bf16(g * sigmoid(g) * u) over gate_up rows [gate | up] of row
+ * stride in_row_stride (>= 2 intermediate), out f16 [rows][intermediate]; r4dx_attn_gate_mul_trellis_bf16:
+ * bf16(attn_out * sigmoid(gate)) over [rows][K]. Byte-identical to the producer followed by the transform.
+ * Throws unless K (intermediate) is a positive multiple of 128, rows is 0..65535 (0: nothing), |prescale_log2|
+ * <= 24 and the pointers are non-null. sigmoid(x) = 1 / (1 + expf(-x)) in fp32 (the device library's expf). */
+void r4dx_silu_mul_trellis_bf16(int64_t gate_up, int64_t rows, int64_t intermediate, int64_t in_row_stride,
+                                int64_t suh, int64_t out, int prescale_log2, int64_t stream);
+void r4dx_attn_gate_mul_trellis_bf16(int64_t attn_out, int64_t gate, int64_t rows, int64_t K, int64_t suh,
+                                     int64_t out, int prescale_log2, int64_t stream);
+/* kernels.h:149-165, 167-179: the two producers quantized like r4dx_trellis_input_i8 (per (row, 128) scales, sa
+ * [K/128][256]) and _i8r (one scale per row, sa [256]): a8 in the A8 layout; rows must be 256. */
+void r4dx_silu_mul_trellis_i8(int64_t gate_up, int64_t rows, int64_t intermediate, int64_t in_row_stride, int64_t suh,
+                              int64_t a8, int64_t sa, int prescale_log2, int64_t stream);
+void r4dx_attn_gate_mul_trellis_i8(int64_t attn_out, int64_t gate, int64_t rows, int64_t K, int64_t suh, int64_t a8,
+                                   int64_t sa, int prescale_log2, int64_t stream);
+void r4dx_silu_mul_trellis_i8r(int64_t gate_up, int64_t rows, int64_t intermediate, int64_t in_row_stride,
+                               int64_t suh, int64_t a8, int64_t sa, int prescale_log2, int64_t stream);
+void r4dx_attn_gate_mul_trellis_i8r(int64_t attn_out, int64_t gate, int64_t rows, int64_t K, int64_t suh, int64_t a8,
+                                    int64_t sa, int prescale_log2, int64_t stream);
+/* kernels.h:90-91 r4dx_silu_mul_wide_bf16: out bf16 [rows][intermediate] = bf16(g * sigmoid(g) * u) over gate_up
+ * rows of stride in_row_stride (rows or intermediate <= 0: nothing) -- the MLP producer alone. */
+void r4dx_silu_mul_wide_bf16(int64_t gate_up, int64_t out, int64_t rows, int64_t intermediate, int64_t in_row_stride,
+                             int64_t stream);
+/* src/model/attention/include/r4dx/model/attention/attn_kernels.h:26-31 r4dx_model_attn_gate_mul_bf16:
+ * out[i] = bf16(attn_out[i] * sigmoid(gate[i])) over n elements (n <= 0: nothing) -- the attention producer. */
+void r4dx_model_attn_gate_mul_bf16(int64_t attn_out, int64_t gate, int64_t out, int64_t n, int64_t stream);
 /* kernels.h:192-197 r4dx_fwht128_f32: in-place unnormalised FWHT of each 128-float block (use_lds
  * accepted: both butterflies are the same fp32 operations in the same order). */
 void r4dx_fwht128_f32(int64_t x, int64_t blocks, int use_lds, int64_t stream);

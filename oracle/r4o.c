@@ -172,6 +172,32 @@ void r4o_fwht128_f64(double* v) {
       }
 }
 
+/* ---- the activation producers in front of the transform ----------------------------------------- */
+/* src/kernels/src/r4dx_kernels.hip:38 Sigmoid: 1 / (1 + expf(-x)) in fp32 (the host libm's expf here; the
+ * GPU's device-library expf may differ from it by an ulp, so the producers are pinned within one bf16 ulp). */
+static float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* src/kernels/src/r4dx_kernels.hip:416-470 SiluMulWideKernel's element (and trellis_transform.hip:119-123):
+ * h = bf16(g * sigmoid(g) * u), g = gate_up[r][i], u = gate_up[r][intermediate + i], two fp32 products in that
+ * order, then nearest-even bf16.  out [rows][intermediate]. */
+void r4o_silu_mul_bf16(const uint16_t* gate_up, int64_t rows, int64_t intermediate, int64_t in_row_stride,
+                       uint16_t* out) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t i = 0; i < intermediate; ++i) {
+      const float g = r4o_bf16_to_f32(gate_up[r * in_row_stride + i]);
+      const float u = r4o_bf16_to_f32(gate_up[r * in_row_stride + intermediate + i]);
+      const float gs = g * sigmoid_f32(g);
+      out[r * intermediate + i] = r4o_f32_to_bf16(gs * u);
+    }
+}
+
+/* trellis_transform.hip:152-170 GateMulTrellisKernel's element (attn_kernels.hip's GateMulKernel):
+ * h = bf16(a * (1 / (1 + expf(-g)))) over n elements. */
+void r4o_attn_gate_mul_bf16(const uint16_t* attn_out, const uint16_t* gate, int64_t n, uint16_t* out) {
+  for (int64_t i = 0; i < n; ++i)
+    out[i] = r4o_f32_to_bf16(r4o_bf16_to_f32(attn_out[i]) * sigmoid_f32(r4o_bf16_to_f32(gate[i])));
+}
+
 /* trellis_ref.hpp:146-148: float(2^s / sqrt(128)), one rounding from double. */
 float r4o_transform_scale(int prescale_log2) {
   return (float)(ldexp(1.0, prescale_log2) / sqrt(128.0));

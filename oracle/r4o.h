@@ -53,6 +53,11 @@ void     r4o_fwht128_f64(double* v);                               /* trellis_re
 float    r4o_transform_scale(int prescale_log2);                   /* trellis_ref.hpp:146-148 */
 /* x: [M][K] bits, x_is_bf16 selects bf16 (the reference's r4dx_trellis_input_bf16) or f16 input;
  * suh fp32 [K]; a: f16 bits [M][K]  (trellis_ref.hpp:150-169, trellis_transform.hip:63-100) */
+/* the activation producers (pinned: sigmoid's closed forms -- 0 -> 1/2, saturation at +-large -- and a float64
+ * restatement within one bf16 ulp, tests/test_oracle.py) */
+void     r4o_silu_mul_bf16(const uint16_t* gate_up, int64_t rows, int64_t intermediate, int64_t in_row_stride,
+                           uint16_t* out);
+void     r4o_attn_gate_mul_bf16(const uint16_t* attn_out, const uint16_t* gate, int64_t n, uint16_t* out);
 void     r4o_transform_input(const uint16_t* x, int x_is_bf16, int64_t M, int64_t K,
                              const float* suh, int prescale_log2, uint16_t* a);
 /* fp64 sums S[m][n] = sum_k A_p(n)[m][k] Q[k][n] (no output transform: the _raw entry's quantity) */

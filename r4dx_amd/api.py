@@ -289,3 +289,71 @@ def trellis_input_i8(x, suh_list, prescale=0, row_scale=False, outs=None, stream
     f = lib().r4dx_trellis_input_i8r if row_scale else lib().r4dx_trellis_input_i8
     f(_p(x), M, K, n, arr(suh_list), arr(a8), arr(sa), prescale, _stream(stream))
     return list(zip(a8, sa))
+
+
+def silu_mul(gate_up, intermediate, out=None, stream=None):
+    """r4dx_silu_mul_wide_bf16: bf16 [rows][intermediate] = bf16(g * sigmoid(g) * u) from gate_up bf16 rows
+    [gate | up] (row stride gate_up.stride(0))."""
+    rows = gate_up.shape[0]
+    if out is None:
+        out = torch.empty((rows, intermediate), dtype=gate_up.dtype, device=gate_up.device)
+    lib().r4dx_silu_mul_wide_bf16(_p(gate_up), _p(out), rows, intermediate, gate_up.stride(0), _stream(stream))
+    return out
+
+
+def attn_gate_mul(attn_out, gate, out=None, stream=None):
+    """r4dx_model_attn_gate_mul_bf16: bf16(attn_out * sigmoid(gate)) elementwise."""
+    if out is None:
+        out = torch.empty_like(attn_out)
+    lib().r4dx_model_attn_gate_mul_bf16(_p(attn_out), _p(gate), _p(out), attn_out.numel(), _stream(stream))
+    return out
+
+
+def _producer_check(K, rows, prescale):
+    if K <= 0 or K % 128 or not 0 <= rows <= 65535 or abs(prescale) > 24:
+        raise ValueError("K must be a positive multiple of 128, rows 0..65535, |prescale| <= 24")
+
+
+def silu_mul_trellis(gate_up, intermediate, suh, prescale=0, quant=None, out=None, stream=None):
+    """The MLP producer fused into mlp.down's input transform: quant None -> f16 A [rows][intermediate]
+    (r4dx_silu_mul_trellis_bf16); 'blk' / 'row' -> (a8, sa) for the int8 GEMM (r4dx_silu_mul_trellis_i8 / _i8r,
+    rows == 256)."""
+    rows, stride = gate_up.shape[0], gate_up.stride(0)
+    _producer_check(intermediate, rows, prescale)
+    if stride < 2 * intermediate:
+        raise ValueError("gate_up's row stride must be >= 2 * intermediate")
+    st = _stream(stream)
+    if quant is None:
+        if out is None:
+            out = torch.empty((rows, intermediate), dtype=torch.float16, device=gate_up.device)
+        lib().r4dx_silu_mul_trellis_bf16(_p(gate_up), rows, intermediate, stride, _p(suh), _p(out), prescale, st)
+        return out
+    if rows != 256:
+        raise ValueError("the int8 forms take exactly 256 rows")
+    a8, sa = out if out is not None else (
+        torch.empty(256 * intermediate, dtype=torch.int8, device=gate_up.device),
+        torch.empty(256 if quant == "row" else (intermediate // 128) * 256, dtype=torch.float32, device=gate_up.device))
+    f = lib().r4dx_silu_mul_trellis_i8r if quant == "row" else lib().r4dx_silu_mul_trellis_i8
+    f(_p(gate_up), rows, intermediate, stride, _p(suh), _p(a8), _p(sa), prescale, st)
+    return a8, sa
+
+
+def attn_gate_mul_trellis(attn_out, gate, suh, prescale=0, quant=None, out=None, stream=None):
+    """The attention output gate fused into attn.o's input transform: quant None -> f16 A [rows][K]
+    (r4dx_attn_gate_mul_trellis_bf16); 'blk' / 'row' -> (a8, sa) (r4dx_attn_gate_mul_trellis_i8 / _i8r)."""
+    rows, K = attn_out.shape
+    _producer_check(K, rows, prescale)
+    st = _stream(stream)
+    if quant is None:
+        if out is None:
+            out = torch.empty((rows, K), dtype=torch.float16, device=attn_out.device)
+        lib().r4dx_attn_gate_mul_trellis_bf16(_p(attn_out), _p(gate), rows, K, _p(suh), _p(out), prescale, st)
+        return out
+    if rows != 256:
+        raise ValueError("the int8 forms take exactly 256 rows")
+    a8, sa = out if out is not None else (
+        torch.empty(256 * K, dtype=torch.int8, device=attn_out.device),
+        torch.empty(256 if quant == "row" else (K // 128) * 256, dtype=torch.float32, device=attn_out.device))
+    f = lib().r4dx_attn_gate_mul_trellis_i8r if quant == "row" else lib().r4dx_attn_gate_mul_trellis_i8
+    f(_p(attn_out), _p(gate), rows, K, _p(suh), _p(a8), _p(sa), prescale, st)
+    return a8, sa

@@ -120,8 +120,8 @@ __device__ __forceinline__ void xq_transform(float x0, float x1, const float* __
 
 // per-(row, 128) scales: one wave per (row, block); the block goes through a wave-private LDS slot to reach
 // q_blk_kernel's lane map (lane l: k = 2 l, 2 l + 1)
-__global__ __launch_bounds__(256) void xq_blk_kernel(const unsigned short* __restrict__ x, int K, int nout, XqOut p,
-                                                     float scale) {
+template <int SRC>
+__global__ __launch_bounds__(256) void xq_blk_kernel(R4XSrc src, int K, int nout, XqOut p, float scale) {
   __shared__ unsigned short buf[4][128];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int nkb = K >> 7;
@@ -129,8 +129,8 @@ __global__ __launch_bounds__(256) void xq_blk_kernel(const unsigned short* __res
   if (id >= 256LL * nkb) return;
   const int row = (int)(id / nkb), kb = (int)(id % nkb);
   const size_t k0 = (size_t)kb * 128;
-  const unsigned short* xr = x + (size_t)row * K + k0;
-  const float x0 = r4_bf16_to_f32(xr[lane]), x1 = r4_bf16_to_f32(xr[lane + 64]);
+  const float x0 = r4_xsrc<SRC, true>(src, row, (long long)k0 + lane);
+  const float x1 = r4_xsrc<SRC, true>(src, row, (long long)k0 + lane + 64);
   for (int o = 0; o < nout; ++o) {
     unsigned short h0, h1;
     xq_transform(x0, x1, p.suh[o], k0, lane, scale, h0, h1);
@@ -155,8 +155,8 @@ __global__ __launch_bounds__(256) void xq_blk_kernel(const unsigned short* __res
 
 // one scale per row: a workgroup (4 waves) per row transforms every block into LDS (f16, [nout][K]), takes the
 // row's amax, then quantizes like q_row_kernel
-__global__ __launch_bounds__(256) void xq_row_kernel(const unsigned short* __restrict__ x, int K, int nout, XqOut p,
-                                                     float scale) {
+template <int SRC>
+__global__ __launch_bounds__(256) void xq_row_kernel(R4XSrc src, int K, int nout, XqOut p, float scale) {
   extern __shared__ unsigned short rowbuf[];
   __shared__ float red[kXqMaxOut][4];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -164,8 +164,8 @@ __global__ __launch_bounds__(256) void xq_row_kernel(const unsigned short* __res
   float amax[kXqMaxOut] = {0.f, 0.f, 0.f};
   for (int kb = w; kb < nkb; kb += 4) {
     const size_t k0 = (size_t)kb * 128;
-    const unsigned short* xr = x + (size_t)row * K + k0;
-    const float x0 = r4_bf16_to_f32(xr[lane]), x1 = r4_bf16_to_f32(xr[lane + 64]);
+    const float x0 = r4_xsrc<SRC, true>(src, row, (long long)k0 + lane);
+    const float x1 = r4_xsrc<SRC, true>(src, row, (long long)k0 + lane + 64);
 #pragma unroll
     for (int o = 0; o < kXqMaxOut; ++o) {
       if (o >= nout) break;
@@ -195,12 +195,39 @@ __global__ __launch_bounds__(256) void xq_row_kernel(const unsigned short* __res
   }
 }
 
+template <int SRC>
+void xq_launch(bool row_scale, const R4XSrc& src, int64_t K, int nout, const XqOut& p, float scale, int64_t stream,
+               const char* entry) {
+  hipStream_t st = (hipStream_t)stream;
+  if (row_scale) {
+    const size_t lds = (size_t)nout * K * 2;
+    // the row's values plus the kernel's 48 static bytes must fit the 160 KiB of a workgroup
+    if (lds > 160 * 1024 - 256) r4d::fail(entry, "nout K 2 bytes must stay below 160 KiB of LDS");
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute((const void*)xq_row_kernel<SRC>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess)
+      r4d::fail(entry, "hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
+    hipLaunchKernelGGL((xq_row_kernel<SRC>), dim3(256), dim3(256), lds, st, src, (int)K, nout, p, scale);
+  } else {
+    const long long waves = 256LL * (K / 128);
+    hipLaunchKernelGGL((xq_blk_kernel<SRC>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, src, (int)K, nout,
+                       p, scale);
+  }
+  r4d::launch_ok(entry);
+}
+
+// float(2^s / sqrt(128)), rounded once from double (trellis_ref.hpp:146-148)
+float xq_scale(int prescale_log2, const char* entry) {
+  if (prescale_log2 < -24 || prescale_log2 > 24) r4d::fail(entry, "|prescale_log2| must be <= 24");
+  return (float)(__builtin_ldexp(1.0, prescale_log2) / __builtin_sqrt(128.0));
+}
+
 void xq_run(bool row_scale, int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh, const int64_t* a8,
             const int64_t* sa, int prescale_log2, int64_t stream, const char* entry) {
   if (M != 256) r4d::fail(entry, "M must be 256 (the A8 layout's rows)");
   if (K <= 0 || K % 128) r4d::fail(entry, "K must be a positive multiple of 128");
   if (nout < 1 || nout > kXqMaxOut) r4d::fail(entry, "nout must be 1..3");
-  if (prescale_log2 < -24 || prescale_log2 > 24) r4d::fail(entry, "|prescale_log2| must be <= 24");
+  const float scale = xq_scale(prescale_log2, entry);
   if (!x || !suh || !a8 || !sa) r4d::fail(entry, "null pointer");
   XqOut p{};
   for (int o = 0; o < nout; ++o) {
@@ -209,24 +236,25 @@ void xq_run(bool row_scale, int64_t x, int64_t M, int64_t K, int nout, const int
     p.a8[o] = (signed char*)a8[o];
     p.sa[o] = (float*)sa[o];
   }
-  // float(2^s / sqrt(128)), rounded once from double (trellis_ref.hpp:146-148)
-  const float scale = (float)(__builtin_ldexp(1.0, prescale_log2) / __builtin_sqrt(128.0));
-  hipStream_t st = (hipStream_t)stream;
-  if (row_scale) {
-    const size_t lds = (size_t)nout * K * 2;
-    // the row's values plus the kernel's 48 static bytes must fit the 160 KiB of a workgroup
-    if (lds > 160 * 1024 - 256) r4d::fail(entry, "nout K 2 bytes must stay below 160 KiB of LDS");
-    if (lds > 64 * 1024 &&
-        hipFuncSetAttribute((const void*)xq_row_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-            hipSuccess)
-      r4d::fail(entry, "hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
-    hipLaunchKernelGGL(xq_row_kernel, dim3(256), dim3(256), lds, st, (const unsigned short*)x, (int)K, nout, p, scale);
-  } else {
-    const long long waves = 256LL * (K / 128);
-    hipLaunchKernelGGL(xq_blk_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, (const unsigned short*)x,
-                       (int)K, nout, p, scale);
-  }
-  r4d::launch_ok(entry);
+  xq_launch<R4_SRC_X>(row_scale, R4XSrc{(const unsigned short*)x, nullptr, (long long)K, 0}, K, nout, p, scale, stream,
+                      entry);
+}
+
+// The fused producers' int8 forms (trellis_transform.hip:971-1000, 1038-1070): the producers' preconditions
+// (K a positive multiple of 128, |prescale_log2| <= 24, non-null suh) plus rows == 256 and non-null a8 and sa.
+void xq_producer(bool row_scale, int SRC, const R4XSrc& src, int64_t rows, int64_t K, int64_t suh, int64_t a8,
+                 int64_t sa, int prescale_log2, int64_t stream, const char* entry) {
+  if (K <= 0 || K % 128) r4d::fail(entry, "K must be a positive multiple of 128");
+  const float scale = xq_scale(prescale_log2, entry);
+  if (!suh) r4d::fail(entry, "suh must be non-null");
+  if (rows != 256) r4d::fail(entry, "rows must be 256 (the int8 A8 layout)");
+  if (!a8 || !sa) r4d::fail(entry, "a8 and sa must be non-null");
+  XqOut p{};
+  p.suh[0] = (const float*)suh;
+  p.a8[0] = (signed char*)a8;
+  p.sa[0] = (float*)sa;
+  if (SRC == R4_SRC_SILU) xq_launch<R4_SRC_SILU>(row_scale, src, K, 1, p, scale, stream, entry);
+  else xq_launch<R4_SRC_GATE>(row_scale, src, K, 1, p, scale, stream, entry);
 }
 
 // plain int8 [N][K] -> the W8 block layout (r4d_trellis_i8_layout.h:24-27): one thread per output
@@ -293,6 +321,42 @@ void r4dx_trellis_input_i8(int64_t x, int64_t M, int64_t K, int nout, const int6
 void r4dx_trellis_input_i8r(int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh, const int64_t* a8,
                             const int64_t* sa, int prescale_log2, int64_t stream) {
   xq_run(true, x, M, K, nout, suh, a8, sa, prescale_log2, stream, "trellis_input_i8r");
+}
+
+// kernels.h:149-163, 167-177: r4dx_silu_mul_trellis_bf16's producer and transform, quantized like
+// r4dx_trellis_input_i8 (per (row, 128) scales) / _i8r (one scale per row); rows must be 256.
+void r4dx_silu_mul_trellis_i8(int64_t gate_up, int64_t rows, int64_t intermediate, int64_t in_row_stride, int64_t suh,
+                              int64_t a8, int64_t sa, int prescale_log2, int64_t stream) {
+  const char* e = "silu_mul_trellis_i8";
+  if (!gate_up) r4d::fail(e, "gate_up is null");
+  if (in_row_stride < 2 * intermediate) r4d::fail(e, "in_row_stride must be >= 2 * intermediate");
+  xq_producer(false, R4_SRC_SILU, R4XSrc{(const unsigned short*)gate_up, nullptr, (long long)in_row_stride,
+                                          (long long)intermediate},
+              rows, intermediate, suh, a8, sa, prescale_log2, stream, e);
+}
+void r4dx_silu_mul_trellis_i8r(int64_t gate_up, int64_t rows, int64_t intermediate, int64_t in_row_stride,
+                               int64_t suh, int64_t a8, int64_t sa, int prescale_log2, int64_t stream) {
+  const char* e = "silu_mul_trellis_i8r";
+  if (!gate_up) r4d::fail(e, "gate_up is null");
+  if (in_row_stride < 2 * intermediate) r4d::fail(e, "in_row_stride must be >= 2 * intermediate");
+  xq_producer(true, R4_SRC_SILU, R4XSrc{(const unsigned short*)gate_up, nullptr, (long long)in_row_stride,
+                                         (long long)intermediate},
+              rows, intermediate, suh, a8, sa, prescale_log2, stream, e);
+}
+// kernels.h:164-165, 178-179: the same for r4dx_attn_gate_mul_trellis_bf16's producer.
+void r4dx_attn_gate_mul_trellis_i8(int64_t attn_out, int64_t gate, int64_t rows, int64_t K, int64_t suh, int64_t a8,
+                                   int64_t sa, int prescale_log2, int64_t stream) {
+  const char* e = "attn_gate_mul_trellis_i8";
+  if (!attn_out || !gate) r4d::fail(e, "attn_out and gate must be non-null");
+  xq_producer(false, R4_SRC_GATE, R4XSrc{(const unsigned short*)attn_out, (const unsigned short*)gate, (long long)K, 0},
+              rows, K, suh, a8, sa, prescale_log2, stream, e);
+}
+void r4dx_attn_gate_mul_trellis_i8r(int64_t attn_out, int64_t gate, int64_t rows, int64_t K, int64_t suh, int64_t a8,
+                                    int64_t sa, int prescale_log2, int64_t stream) {
+  const char* e = "attn_gate_mul_trellis_i8r";
+  if (!attn_out || !gate) r4d::fail(e, "attn_out and gate must be non-null");
+  xq_producer(true, R4_SRC_GATE, R4XSrc{(const unsigned short*)attn_out, (const unsigned short*)gate, (long long)K, 0},
+              rows, K, suh, a8, sa, prescale_log2, stream, e);
 }
 // plain int8 [N][K] -> W8 block layout (N K bytes), once per weight
 void r4d_i8_pack_w(int64_t wp, int64_t w8, int N, int K, int64_t stream) {

@@ -66,6 +66,37 @@ __device__ __forceinline__ float r4_bf16_to_f32(unsigned short h) {
   return __builtin_bit_cast(float, (unsigned)h << 16);
 }
 
+// ---- the activation producers in front of a trellis linear's input transform ----------------------------
+// sigmoid(x) = 1 / (1 + e^-x) in fp32: the device library's expf, a correctly rounded divide (the reference's
+// element, src/kernels/src/r4dx_kernels.hip:38, src/kernels/src/trellis_transform.hip:106).
+__device__ __forceinline__ float r4_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+// Where a transform reads its input x[row][k] (k inside the row):
+//   R4_SRC_X    x itself (bf16 or f16 bits), rows ld apart;
+//   R4_SRC_SILU bf16(g * sigmoid(g) * u) with g = p0[row ld + k], u = p0[row ld + off + k] (the MLP's
+//               [gate | up] rows; the two products rounded to fp32 in that order, then to bf16 by RNE);
+//   R4_SRC_GATE bf16(a * sigmoid(g)) with a = p0[row ld + k], g = p1[row ld + k] (attention's output gate).
+// The producers' values are the bf16 numbers a separate producer kernel would have stored.
+constexpr int R4_SRC_X = 0, R4_SRC_SILU = 1, R4_SRC_GATE = 2;
+struct R4XSrc {
+  const unsigned short* p0;
+  const unsigned short* p1;
+  long long ld, off;
+};
+// x[row][k] of a transform's input source (see R4XSrc), as fp32
+template <int SRC, bool BF16>
+__device__ __forceinline__ float r4_xsrc(const R4XSrc& s, long long row, long long k) {
+  const long long i = row * s.ld + k;
+  if constexpr (SRC == R4_SRC_X) {
+    return BF16 ? r4_bf16_to_f32(s.p0[i]) : r4_f16_to_f32(s.p0[i]);
+  } else if constexpr (SRC == R4_SRC_SILU) {
+    const float g = r4_bf16_to_f32(s.p0[i]), u = r4_bf16_to_f32(s.p0[i + s.off]);
+    return r4_bf16_to_f32(r4_bf16_rn(g * r4_sigmoid(g) * u));
+  } else {
+    const float a = r4_bf16_to_f32(s.p0[i]), g = r4_bf16_to_f32(s.p1[i]);
+    return r4_bf16_to_f32(r4_bf16_rn(a * r4_sigmoid(g)));
+  }
+}
+
 // ---- trellis value path -------------------------------------------------------------------------
 #define R4_SAD_SEED 0x64006400u     // f16 1024.0 in both halves
 #define R4_KINV2 0x1EEE1EEEu

@@ -65,6 +65,14 @@ SIGS = {
     "r4dx_trellis_input_bf16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
     "r4dx_trellis_input_f16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
     "r4dx_fwht128_f32": (None, [I64, I64, I32, I64]),
+    "r4dx_silu_mul_trellis_bf16": (None, [I64] * 6 + [I32, I64]),
+    "r4dx_attn_gate_mul_trellis_bf16": (None, [I64] * 6 + [I32, I64]),
+    "r4dx_silu_mul_trellis_i8": (None, [I64] * 7 + [I32, I64]),
+    "r4dx_attn_gate_mul_trellis_i8": (None, [I64] * 7 + [I32, I64]),
+    "r4dx_silu_mul_trellis_i8r": (None, [I64] * 7 + [I32, I64]),
+    "r4dx_attn_gate_mul_trellis_i8r": (None, [I64] * 7 + [I32, I64]),
+    "r4dx_silu_mul_wide_bf16": (None, [I64] * 6),
+    "r4dx_model_attn_gate_mul_bf16": (None, [I64] * 5),
 }
 
 _lib = None

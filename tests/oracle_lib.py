@@ -38,6 +38,8 @@ _SIGS = {
     "r4o_fwht128_f64": (None, [P]),
     "r4o_transform_scale": (C.c_float, [I32]),
     "r4o_transform_input": (None, [P, I32, I64, I64, P, I32, P]),
+    "r4o_silu_mul_bf16": (None, [P, I64, I64, I64, P]),
+    "r4o_attn_gate_mul_bf16": (None, [P, P, I64, P]),
     "r4o_raw_sums_f64": (None, [P, P, I64, I64, I64, I64, P, P, I32]),
     "r4o_linear_from_a": (None, [P, P, I64, I64, I64, I64, P, P, I32, P, I32]),
     "r4o_epilogue_from_raw": (None, [P, I64, I64, P, C.c_float, P]),

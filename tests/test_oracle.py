@@ -266,3 +266,49 @@ def test_argmax_order(olib):
     i, v = am([-np.inf, np.nan, -np.inf])
     assert i == 0 and v == -np.inf
     assert am([np.nan, 5, 5, np.inf, np.inf])[0] == 3
+
+
+# ---- the activation producers (r4o_silu_mul_bf16, r4o_attn_gate_mul_bf16) ---------------------------------
+def _bf16(x):
+    return O.f32_to_bf16_bits(np.asarray(x, np.float32))
+
+
+def test_producers_closed_forms(olib):
+    """sigmoid(0) = 1/2 exactly, sigmoid saturates to 1 at +100 (e^-100 is below an fp32 ulp of 1) and to 0
+    at -100 (e^100 overflows): silu(g) u and a sigmoid(g) are then bf16(g u), +-0, bf16(a / 2), bf16(a)."""
+    g = np.array([0.0, 100.0, -100.0, 0.0, 100.0, -100.0], np.float32)
+    u = np.array([3.0, 1.5, 7.0, -2.0, -0.375, -5.0], np.float32)
+    gu = np.concatenate([_bf16(g), _bf16(u)]).astype(np.uint16)
+    out = np.empty(6, np.uint16)
+    olib.r4o_silu_mul_bf16(ptr(gu), 1, 6, 12, ptr(out))
+    got = O.bf16_bits_to_f32(out)
+    want = np.array([0.0, 150.0, -0.0, -0.0, -37.5, 0.0], np.float32)
+    assert np.array_equal(got, want) and np.array_equal(np.signbit(got), np.signbit(want))
+    a = np.array([3.0, -1.25, 6.5, 1e-3], np.float32)
+    gg = np.array([0.0, 0.0, 100.0, -100.0], np.float32)
+    outg = np.empty(4, np.uint16)
+    olib.r4o_attn_gate_mul_bf16(ptr(_bf16(a)), ptr(_bf16(gg)), 4, ptr(outg))
+    assert np.array_equal(O.bf16_bits_to_f32(outg), O.bf16_bits_to_f32(_bf16([1.5, -0.625, 6.5, 0.0])))
+
+
+def test_producers_match_float64(olib):
+    """Random gate/up and attention values against a float64 restatement (g / (1 + e^-g) * u, a / (1 + e^-g)):
+    within one bf16 ulp everywhere, and the rows, the [gate | up] split and the row stride are honoured."""
+    rng = np.random.default_rng(7)
+    rows, inter, stride = 3, 384, 2 * 384 + 64
+    gu = _bf16(rng.normal(0, 3, (rows, stride)).astype(np.float32))
+    out = np.empty((rows, inter), np.uint16)
+    olib.r4o_silu_mul_bf16(ptr(gu), rows, inter, stride, ptr(out))
+    g = O.bf16_bits_to_f32(gu[:, :inter]).astype(np.float64)
+    u = O.bf16_bits_to_f32(gu[:, inter:2 * inter]).astype(np.float64)
+    ref = g / (1.0 + np.exp(-g)) * u
+    got = O.bf16_bits_to_f32(out).astype(np.float64)
+    ulp = np.abs(O.bf16_bits_to_f32(_bf16(ref)).astype(np.float64)) * 2.0**-7 + 1e-30
+    assert np.all(np.abs(got - ref) <= ulp)
+    a = _bf16(rng.normal(0, 2, 1000).astype(np.float32))
+    gg = _bf16(rng.normal(0, 4, 1000).astype(np.float32))
+    outg = np.empty(1000, np.uint16)
+    olib.r4o_attn_gate_mul_bf16(ptr(a), ptr(gg), 1000, ptr(outg))
+    refg = O.bf16_bits_to_f32(a).astype(np.float64) / (1.0 + np.exp(-O.bf16_bits_to_f32(gg).astype(np.float64)))
+    gotg = O.bf16_bits_to_f32(outg).astype(np.float64)
+    assert np.all(np.abs(gotg - refg) <= np.abs(refg) * 2.0**-7 + 1e-30)
