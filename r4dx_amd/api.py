@@ -3,6 +3,7 @@ library's own _check entry (or the same rules) first, so an illegal shape raises
 instead of an uncaught C++ exception crossing ctypes."""
 import ctypes as C
 
+import numpy as np
 import torch
 
 from .loader import lib
@@ -357,3 +358,30 @@ def attn_gate_mul_trellis(attn_out, gate, suh, prescale=0, quant=None, out=None,
     f = lib().r4dx_attn_gate_mul_trellis_i8r if quant == "row" else lib().r4dx_attn_gate_mul_trellis_i8
     f(_p(attn_out), _p(gate), rows, K, _p(suh), _p(a8), _p(sa), prescale, st)
     return a8, sa
+
+
+def trellis_linear_to_device(lin, device):
+    """A container.TrellisLinear's arrays as device tensors: words int32, suh fp32 per part, svh fp32."""
+    return {"words": torch.from_numpy(lin.words.view(np.int32)).to(device),
+            "suh": [torch.from_numpy(s).to(device) for s in lin.suh],
+            "svh": torch.from_numpy(lin.svh).to(device)}
+
+
+def trellis_linear(x, lin, dev_t, out_scale=None, stream=None):
+    """y bf16 [M][N] = the trellis linear `lin` (container.TrellisLinear, its device tensors dev_t) of x bf16
+    [M][K]: the input transform (one output per part, the linear's prescale), then r4d_gemm_trellis_nt_m64
+    (M <= 64) or r4d_gemm_trellis_nt_m256 (M = 128 or 256), a two-part linear split at its first part. The
+    default out_scale is the engine's float(2^-prescale / sqrt(128)) (src/model/linear.cpp:1074)."""
+    M, K = x.shape
+    if out_scale is None:
+        out_scale = float(np.float32(np.ldexp(1.0, -lin.prescale_log2) / np.sqrt(128.0)))
+    if K != lin.K:
+        raise ValueError(f"x has K = {K}, the linear {lin.base} K = {lin.K}")
+    a = trellis_input(x, dev_t["suh"], lin.prescale_log2, stream=stream)
+    a1 = a[1] if len(a) > 1 else None
+    n_split = lin.parts[0] if lin.parts else None
+    if M <= 64:
+        return trellis_gemm_m64(a[0], dev_t["words"], dev_t["svh"], lin.K, lin.N, lin.KB, a1=a1, n_split=n_split,
+                                out_scale=out_scale, stream=stream)
+    return trellis_gemm_m256(a[0], dev_t["words"], dev_t["svh"], lin.K, lin.N, lin.KB, a1=a1, n_split=n_split,
+                             out_scale=out_scale, stream=stream)
