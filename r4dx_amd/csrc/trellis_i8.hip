@@ -738,7 +738,7 @@ void r4d_gemm_i8_dense_raw(int64_t a8, int64_t w8, int64_t c, int64_t ws, int64_
 int r4d_mi355x_i8_skg(int K, int N) {
   const int G = N / 128, nkb = K / 128;
   int best = 1;
-  for (int d = 1; d <= 16; ++d) {
+  for (int d = 1; d <= 8; d *= 2) {         // the split counts r4d_gemm_trellis_nt_i8_check allows
     if (nkb % d || nkb / d < 8) continue;
     best = d;
     if ((long long)G * d >= 128) break;

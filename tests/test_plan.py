@@ -1,0 +1,43 @@
+"""The MI355X tuning plan (r4dx_amd/plan.py): refusals with a reason (the rules of src/model/linear.cpp:680-766),
+the row-identity rule (every M <= 16 the same knobs), the M = 64 band on the M = 256 plan's (SK = 1, SKG), and
+every accepted plan legal by the kernels' own _check. CPU only (the planners and checks launch nothing); the
+GPU identity of an M = 256 launch with the M = 64 band's rows is tests/test_m256_gpu.py's."""
+import pytest
+
+from r4dx_amd import plan
+from r4dx_amd import workloads as WL
+
+SHAPES = [(N, K) for _, K, N in WL.LAYER_SHAPES] + [(34816, 5120)]
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+@pytest.mark.parametrize("kb", [4, 5])
+def test_plans_of_the_config1_shapes(N, K, kb):
+    decode = [plan.linear_tuning(N, K, kb, M) for M in range(1, 17)]
+    assert all(p.ok for p in decode) and len({(p.SK, p.SKG) for p in decode}) == 1
+    band = [plan.linear_tuning(N, K, kb, M) for M in (17, 32, 33, 64)]
+    m256 = plan.plan_trellis_m256(N, K, kb)
+    assert m256.ok and all(p.ok and (p.SK, p.SKG) == (1, m256.SKG) for p in band)
+    i8 = plan.plan_trellis_i8(N, K, kb)
+    assert i8.ok and i8.skw in (2, 4, 8) and (K // 128) % (i8.skw * i8.SKG) == 0
+
+
+def test_two_part_plans():
+    assert plan.linear_tuning(34816, 5120, 4, 1, parts=2, part_n0=17408).ok
+    assert plan.plan_trellis_m256(34816, 5120, 4, parts=2, part_n0=17408).ok
+    assert plan.plan_trellis_i8(34816, 5120, 4, parts=2, part_n0=17408, coarse=True).kernel == "i8c"
+
+
+@pytest.mark.parametrize("f,args,why", [
+    (plan.plan_trellis_m256, (5120, 5120, 3), "KB"),
+    (plan.plan_trellis_m256, (5120, 5100, 4), "128-blocks"),
+    (plan.plan_trellis_m256, (5120, 5120, 4, 3, 128), "parts"),
+    (plan.plan_trellis_m256, (5120, 5120, 4, 2, 5120), "part boundary"),
+    (plan.plan_trellis_m256, (5120, 5120, 4, 2, 200), "part boundary"),
+    (plan.plan_trellis_i8, (5120, 5120, 6), "KB"),
+    (plan.linear_tuning, (5120, 5120, 4, 65), "M must be"),
+    (plan.linear_tuning, (5120, 5120, 2, 1), "KB"),
+])
+def test_refusals_name_the_rule(f, args, why):
+    p = f(*args)
+    assert not p.ok and why in p.why
