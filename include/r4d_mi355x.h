@@ -188,6 +188,25 @@ void r4dx_trellis_input_bf16(int64_t x, int64_t M, int64_t K, int nout, const in
 /* The same for an f16 x (fp16 activations); no reference counterpart, same contract. */
 void r4dx_trellis_input_f16(int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh,
                             const int64_t* out, int prescale_log2, int64_t stream);
+/* r4d.h:425-454 weight fake-quant, a measurement hook: r4d_gemm_trellis_nt_m64 / _raw / r4d_gemm_trellis_nt_m256
+ * with every decoded weight w rounded, right before the MFMA, to f16(clamp(rint(w (1 / s)), -127, 127) s) (all but
+ * the last rounding in fp32) under its column's scale s of a group of 2^gsh k-tiles. The table [K / 16 >> gsh][N]
+ * (r4d_trellis_wscale_count floats) holds s = max|Q| / 127 per (group, column), 1 for an all-zero group, built by
+ * r4d_trellis_wscale_f32 from the pair-grid words with the GEMM's own decode (N a multiple of 32, KB 4 or 5).
+ * The _wq entries take the plain entry's arguments and legality plus the table (null throws) and gsh (1, 2 or 3,
+ * 16 << gsh dividing K); KB 4 or 5. The M = 256 form equals the M = 64 form at SK = 1 and the same SKG, bit for bit. */
+size_t r4d_trellis_wscale_count(int K, int N, int gsh);
+void r4d_trellis_wscale_f32(int64_t w, int64_t scale, int K, int N, int KB, int gsh, int64_t stream);
+void r4d_gemm_trellis_nt_m64_wq(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c, int64_t ws,
+                                int64_t tickets, int M, int K, int N, int KB, int WV, int SK, int MT, int NP, int SKG,
+                                int U, int NT, float out_scale, int64_t wscale, int gsh, int64_t stream);
+void r4d_gemm_trellis_nt_m64_raw_wq(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t c, int64_t ws,
+                                    int64_t tickets, int M, int K, int N, int KB, int WV, int SK, int MT, int NP,
+                                    int SKG, int U, int NT, int64_t wscale, int gsh, int64_t stream);
+void r4d_gemm_trellis_nt_m256_wq(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
+                                 int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SK, int NP,
+                                 int SKG, int U, float out_scale, int64_t stream, int skw, int64_t wscale,
+                                 int gsh);
 /* kernels.h:130-147 the fused producers: r4dx_trellis_input_bf16 (nout = 1) over the bf16 value a producer kernel
  * would have stored -- r4dx_silu_mul_trellis_bf16: bf16(g * sigmoid(g) * u) over gate_up rows [gate | up] of row
  * stride in_row_stride (>= 2 intermediate), out f16 [rows][intermediate]; r4dx_attn_gate_mul_trellis_bf16:

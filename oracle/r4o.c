@@ -551,3 +551,28 @@ int32_t r4o_argmax_f32(const float* x, int64_t n, float* best_val) {
   if (best_val) *best_val = bv;
   return bi;
 }
+
+/* ---- weight fake-quant (src/model/fake_quant_w.h:96-140) ----------------------------------------------------
+ * A group is `group` consecutive k of one column n of Q; s = max|w| / 127 in fp32 (1 for an all-zero group);
+ * a value becomes f16(clamp(rint(w * (1 / s)), -127, 127) * s), every step but the last in fp32 (nearbyintf
+ * under the default rounding mode is round half to even). */
+void r4o_wq_table(const uint16_t* q, int64_t K, int64_t N, int group, float* t) {
+  for (int64_t g = 0; g < K / group; ++g)
+    for (int64_t n = 0; n < N; ++n) {
+      float amax = 0.0f;
+      for (int i = 0; i < group; ++i) amax = fmaxf(amax, fabsf(r4o_f16_to_f32(q[(g * group + i) * N + n])));
+      t[g * N + n] = amax > 0.0f ? amax / 127.0f : 1.0f;
+    }
+}
+
+void r4o_wq_apply(const uint16_t* q, int64_t K, int64_t N, int group, const float* t, uint16_t* out) {
+  for (int64_t k = 0; k < K; ++k)
+    for (int64_t n = 0; n < N; ++n) {
+      const float s = t[(k / group) * N + n];
+      const float rs = 1.0f / s;
+      float v = nearbyintf(r4o_f16_to_f32(q[k * N + n]) * rs);
+      v = fminf(fmaxf(v, -127.0f), 127.0f);
+      const float p = v * s;
+      out[k * N + n] = r4o_f32_to_f16(p);
+    }
+}

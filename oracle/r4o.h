@@ -113,6 +113,14 @@ void     r4o_w4_dequant(const uint32_t* wq, const uint32_t* wsz, int N, int K, i
 void     r4o_w4_gemm_ref(const uint16_t* a, const uint32_t* wq, const uint32_t* wsz, int M, int N,
                          int K, int group, double* y, int nthreads);
 
+/* ---- weight fake-quant (src/model/fake_quant_w.h:96-140; pinned: bit-equality with that header's
+ * FakeQuantWTableRef / FakeQuantWApplyRef through oracle/_ref, all-zero groups -> 1, int8-grid fixed points,
+ * ties to even, the s / 2 error bound, tests/test_oracle.py) ------------------------------------------ */
+/* q f16 bits [K][N] -> t [K/group][N] */
+void     r4o_wq_table(const uint16_t* q, int64_t K, int64_t N, int group, float* t);
+/* q -> f16 bits of the rounded weight Q' [K][N] */
+void     r4o_wq_apply(const uint16_t* q, int64_t K, int64_t N, int group, const float* t, uint16_t* out);
+
 /* ---- argmax (src/kernels/include/r4dx/kernels/argmax_ref.hpp:22-41) ------------------------- */
 int32_t  r4o_argmax_f32(const float* x, int64_t n, float* best_val);
 

@@ -6,6 +6,7 @@
 //   tests/kernels/int8_gemm_proto_ref.h                  int8 quantizers and reference GEMM
 //   src/convert/include/r4dx_convert/quant_int4.hpp      w4a16 quantizer and packers
 //   src/kernels/include/r4dx/kernels/argmax_ref.hpp      argmax order
+//   src/model/fake_quant_w.h                             weight fake-quant table and rounding
 #include <cstring>
 #include <vector>
 
@@ -13,6 +14,7 @@
 #include "int8_gemm_proto_ref.h"
 #include "r4dx_convert/quant_int4.hpp"
 #include "r4dx/kernels/argmax_ref.hpp"
+#include "fake_quant_w.h"
 
 extern "C" {
 
@@ -98,6 +100,21 @@ int32_t ref_argmax(const float* x, int64_t n, float* v) {
   auto p = r4dx::kernels::ArgmaxDirectRef(x, n);
   if (v) *v = p.v;
   return p.i;
+}
+
+// weight fake-quant: Q f16 bits widened to fp32, as the reference's own test feeds it
+void ref_wq_table(const uint16_t* q, int64_t K, int64_t N, int group, float* t) {
+  std::vector<float> qf(static_cast<size_t>(K * N));
+  for (size_t i = 0; i < qf.size(); ++i) qf[i] = r4dx::core::F16ToFloat(q[i]);
+  auto v = r4dx::model::FakeQuantWTableRef(qf.data(), K, N, group);
+  std::memcpy(t, v.data(), v.size() * 4);
+}
+void ref_wq_apply(const uint16_t* q, int64_t K, int64_t N, int group, const float* t, float* out) {
+  std::vector<float> qf(static_cast<size_t>(K * N));
+  for (size_t i = 0; i < qf.size(); ++i) qf[i] = r4dx::core::F16ToFloat(q[i]);
+  std::vector<float> tab(t, t + static_cast<size_t>(K / group) * static_cast<size_t>(N));
+  auto v = r4dx::model::FakeQuantWApplyRef(qf.data(), K, N, group, tab);
+  std::memcpy(out, v.data(), v.size() * 4);
 }
 
 uint16_t ref_f32_to_f16(float f) { return r4dx::core::FloatToF16(f); }

@@ -26,16 +26,29 @@ class TicketBuffer:
         self.t = torch.zeros(max(1, N // 128), dtype=torch.int32, device=device)
 
 
+def _wq_args(wq, K, KB):
+    """(table pointer, gsh) of a _wq call, with the entries' own rules raised here as ValueError."""
+    tab, gsh = wq
+    if tab is None:
+        raise ValueError("the _wq entry needs a scale table (trellis_wscale)")
+    if gsh not in (1, 2, 3) or K % (16 << gsh):
+        raise ValueError("gsh must be 1, 2 or 3 with 16 << gsh dividing K")
+    if KB not in (4, 5):
+        raise ValueError("KB must be 4 or 5")
+    return _p(tab), gsh
+
+
 def trellis_gemv_skg(K, N, KB):
     return lib().r4d_mi355x_trellis_gemv_skg(K, N, KB)
 
 
 def trellis_gemm_m64(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out=None, ws=None,
-                     tickets=None, out_scale=1.0, raw=False, stream=None, sk=0, clk=None):
+                     tickets=None, out_scale=1.0, raw=False, stream=None, sk=0, clk=None, wq=None):
     """C = r4d_gemm_trellis_nt_m64 (bf16 [M][N]) or, raw=True, its _raw fp32 A @ Q. sk = 1: the one-wave-per-
     pair summation order that r4d_gemm_trellis_nt_m256 reproduces bit for bit. clk (raw only): an int64
     device tensor of 4 that receives workgroup (0, 0)'s shader clock and wall clock at entry and at the end
-    of its own work."""
+    of its own work. wq = (table, gsh): the _wq entry, every decoded weight fake-quantized to int8 under the
+    table of trellis_wscale (not with clk)."""
     L = lib()
     M = a0.shape[0]
     skg = trellis_gemv_skg(K, N, KB) if skg is None else skg
@@ -52,7 +65,17 @@ def trellis_gemm_m64(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out=
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32 if raw else torch.bfloat16, device=a0.device)
     st = _stream(stream)
-    if raw:
+    if wq is not None:
+        if clk is not None:
+            raise ValueError("the _wq entries take no clock probe")
+        tab, gsh = _wq_args(wq, K, KB)
+        if raw:
+            L.r4d_gemm_trellis_nt_m64_raw_wq(_p(a0), _p(a1), n_split, _p(w), _p(out), _p(ws), _p(tickets),
+                                             M, K, N, KB, 0, sk, 0, 0, skg, 0, 0, tab, gsh, st)
+        else:
+            L.r4d_gemm_trellis_nt_m64_wq(_p(a0), _p(a1), n_split, _p(w), _p(svh), _p(out), _p(ws), _p(tickets),
+                                         M, K, N, KB, 0, sk, 0, 0, skg, 0, 0, float(out_scale), tab, gsh, st)
+    elif raw:
         L.r4d_gemm_trellis_nt_m64_raw(_p(a0), _p(a1), n_split, _p(w), _p(out), _p(ws), _p(tickets),
                                       M, K, N, KB, 0, sk, 0, 0, skg, 0, 0, _p(clk), st)
     else:
@@ -66,8 +89,9 @@ def trellis_m256_skg(K, N, KB):
 
 
 def trellis_gemm_m256(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out=None, ws=None,
-                      tickets=None, out_scale=1.0, raw=False, stream=None):
-    """C = r4d_gemm_trellis_nt_m256 (bf16 [M][N], M = 128 or 256) or, raw=True, fp32 A @ Q."""
+                      tickets=None, out_scale=1.0, raw=False, stream=None, wq=None):
+    """C = r4d_gemm_trellis_nt_m256 (bf16 [M][N], M = 128 or 256) or, raw=True, fp32 A @ Q. wq = (table, gsh):
+    r4d_gemm_trellis_nt_m256_wq (bf16 only)."""
     L = lib()
     M = a0.shape[0]
     skg = trellis_m256_skg(K, N, KB) if skg is None else skg
@@ -83,12 +107,31 @@ def trellis_gemm_m256(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32 if raw else torch.bfloat16, device=a0.device)
     st = _stream(stream)
-    if raw:
+    if wq is not None:
+        if raw:
+            raise ValueError("r4d_gemm_trellis_nt_m256_wq has no raw form")
+        tab, gsh = _wq_args(wq, K, KB)
+        L.r4d_gemm_trellis_nt_m256_wq(_p(a0), _p(a1), n_split, _p(w), _p(svh), _p(out), _p(ws), _p(tickets),
+                                      M, K, N, KB, 0, 0, skg, 0, float(out_scale), st, 0, tab, gsh)
+    elif raw:
         L.r4d_gemm_trellis_nt_m256_raw(_p(a0), _p(a1), n_split, _p(w), _p(out), _p(ws), _p(tickets),
                                        M, K, N, KB, skg, st)
     else:
         L.r4d_gemm_trellis_nt_m256(_p(a0), _p(a1), n_split, _p(w), _p(svh), _p(out), _p(ws), _p(tickets),
                                    M, K, N, KB, 0, 0, skg, 0, float(out_scale), st, 0)
+    return out
+
+
+def trellis_wscale(w, K, N, KB, gsh, out=None, stream=None):
+    """The fake-quant scale table [K / 16 >> gsh][N] of r4d_trellis_wscale_f32 (fp32 max|Q| / 127 per column
+    and group of 2^gsh k-tiles, 1 for an all-zero group)."""
+    L = lib()
+    n = L.r4d_trellis_wscale_count(K, N, gsh)
+    if n == 0 or KB not in (4, 5) or N % 32 or K % (16 << gsh) or (K // 16) % 4:
+        raise ValueError("trellis_wscale: KB 4 or 5, N a multiple of 32, gsh 1..3, 16 << gsh and 64 dividing K")
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=w.device)
+    L.r4d_trellis_wscale_f32(_p(w), _p(out), K, N, KB, gsh, _stream(stream))
     return out
 
 

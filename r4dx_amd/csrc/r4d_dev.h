@@ -66,6 +66,34 @@ __device__ __forceinline__ float r4_bf16_to_f32(unsigned short h) {
   return __builtin_bit_cast(float, (unsigned)h << 16);
 }
 
+// ---- weight fake-quant (a measurement hook: the _wq entries) ------------------------------------------------
+// Two decoded f16 weights of one column under its group scale s, the reference's rounding
+// (third_party/libr4d/r4d_trellis_dq.h:438-470, src/model/fake_quant_w.h:103-118): rs = 1 / s (IEEE division),
+// q = clamp(rint(w rs), -127, 127), the fp32 product q s, then one f16 rounding (the empty asm in r4_f16_rn keeps
+// the product an fp32 value instead of a fused f16 conversion).
+__device__ __forceinline__ unsigned r4_wq_round2(unsigned d, float rs, float s) {
+  unsigned o = 0;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const float w = r4_f16_to_f32((unsigned short)(d >> (16 * hh)));
+    float q = __builtin_rintf(w * rs);
+    q = __builtin_fminf(__builtin_fmaxf(q, -127.0f), 127.0f);
+    o |= (unsigned)r4_f16_rn(q * s) << (16 * hh);
+  }
+  return o;
+}
+// d[cs][h][j] of a decode lane (columns 8 cs + c of its tile) under the column scales s[cs]
+__device__ __forceinline__ void r4_wq_apply(unsigned (&d)[2][2][4], const float (&s)[2]) {
+#pragma unroll
+  for (int cs = 0; cs < 2; ++cs) {
+    const float rs = 1.0f / s[cs];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d[cs][h][j] = r4_wq_round2(d[cs][h][j], rs, s[cs]);
+  }
+}
+
 // ---- the activation producers in front of a trellis linear's input transform ----------------------------
 // sigmoid(x) = 1 / (1 + e^-x) in fp32: the device library's expf, a correctly rounded divide (the reference's
 // element, src/kernels/src/r4dx_kernels.hip:38, src/kernels/src/trellis_transform.hip:106).

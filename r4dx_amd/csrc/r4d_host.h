@@ -63,4 +63,7 @@ struct r4d_gemv_args {
   // the _raw entry's clock probe: 4 uint64 (shader clock, wall clock at entry; the same at the end of
   // workgroup (0, 0)'s own work), or 0
   int64_t clk;
+  // the _wq measurement entries: the weight scale table [K / 16 >> wq_gsh][N] (0: off) and its group shift
+  int64_t wsc;
+  int wq_gsh;
 };

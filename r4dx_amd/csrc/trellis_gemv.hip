@@ -92,13 +92,13 @@ constexpr int kRedRows = 4;          // rows of the final slice sum per pass
 // XF > 0: A0 is the raw input x [M][K] (XF 1: f16, 2: bf16) and the workgroup stages its own slice of the
 // transformed A = f16(FWHT128(fp32(x) * suh) * xscale) (suh0 / suh1 by column part) straight into LDS --
 // the arithmetic of r4dx_trellis_input_*, so A is bit-identical to the unfused path's.
-template <int KB, int MT, int NPW, int SK, bool ALDS, int XF>
+template <int KB, int MT, int NPW, int SK, bool ALDS, int XF, bool WQ = false>
 __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     const unsigned short* __restrict__ A0, const unsigned short* __restrict__ A1, int n_split,
     const unsigned* __restrict__ W, const float* __restrict__ svh, void* __restrict__ Cv,
     float* __restrict__ ws, unsigned* __restrict__ tickets, int M, int K, int N, int SKG, int full,
     float out_scale, const float* __restrict__ suh0, const float* __restrict__ suh1, float xscale,
-    unsigned long long* __restrict__ clk) {
+    unsigned long long* __restrict__ clk, const float* __restrict__ wsc, int wq_gsh) {
   constexpr int PF = 4;
   constexpr int NT = 64 * NPW * SK;
   constexpr int NW = NPW * SK;                 // waves
@@ -191,6 +191,17 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     unsigned d[2][2][4];
     if constexpr (XF == 0) {
       r4_decode<KB>(s.w.w, d);
+      if constexpr (WQ) {
+        // the _wq measurement: this lane's k-tile and two columns under their group scales
+        const int kt = kt0 + (st_beg + sidx) * 4 + q;
+        float sc[2] = {1.0f, 1.0f};
+        if (kt < KT) {
+          const size_t row = (size_t)(kt >> wq_gsh) * N + (size_t)pair * 32 + 16 * t + c;
+          sc[0] = wsc[row];
+          sc[1] = wsc[row + 8];
+        }
+        r4_wq_apply(d, sc);
+      }
     } else {
       // the fused-transform form takes the history word from lane c - 1 through the LDS crossbar (ds_bpermute,
       // no VALU): measured 3 % faster there, while in the plain form the load is faster
@@ -473,6 +484,50 @@ __global__ __launch_bounds__(256) void tq_reconstruct_kernel(const unsigned* __r
   }
 }
 
+// The _wq entries' scale table [K / 16 >> gsh][N] (r4d.h:433-436): s = max|Q| / 127 (fp32 division; 1 for an
+// all-zero group) over each column's 16 2^gsh values of a group of 2^gsh k-tiles, from the GEMM's own decode. One
+// wave per (tile pair, block of max(4, 2^gsh) k-tiles); a lane takes the amax of its 16 values per column, the
+// lanes of one group meet by shuffles.
+template <int KB>
+__global__ __launch_bounds__(256) void tq_wscale_kernel(const unsigned* __restrict__ W, float* __restrict__ table,
+                                                        int K, int N, int gsh) {
+  const int lane = threadIdx.x & 63;
+  const int KT = K >> 4, ktb = max(4, 1 << gsh), nblk = KT / ktb;
+  const long long id = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (id >= (long long)(N >> 5) * nblk) return;
+  const int pair = (int)(id / nblk), blk = (int)(id - (long long)pair * nblk);
+  const int q = lane >> 4, t = (lane >> 3) & 1, c = lane & 7;
+  float m[2] = {0.f, 0.f};
+  for (int st = 0; st < ktb / 4; ++st) {
+    const int kt = blk * ktb + st * 4 + q;
+    Words<KB> w;
+    load_words_ptr<KB>(w, W + ((size_t)pair * KT + kt) * (16 * KB), t, c);
+    unsigned d[2][2][4];
+    r4_decode<KB>(w.w, d);
+#pragma unroll
+    for (int cs = 0; cs < 2; ++cs)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const unsigned v = d[cs][h][j];
+          m[cs] = __builtin_fmaxf(m[cs], __builtin_fmaxf(__builtin_fabsf(r4_f16_to_f32((unsigned short)(v & 0xFFFFu))),
+                                                         __builtin_fabsf(r4_f16_to_f32((unsigned short)(v >> 16)))));
+        }
+  }
+  // a group spans k-tile lanes q ^ 1 (gsh 1) or all four (gsh >= 2)
+#pragma unroll
+  for (int cs = 0; cs < 2; ++cs) {
+    m[cs] = __builtin_fmaxf(m[cs], __shfl_xor(m[cs], 16, 64));
+    if (gsh >= 2) m[cs] = __builtin_fmaxf(m[cs], __shfl_xor(m[cs], 32, 64));
+  }
+  if ((q & ((1 << min(gsh, 2)) - 1)) != 0) return;
+  const int g = (blk * ktb + q) >> gsh;
+#pragma unroll
+  for (int cs = 0; cs < 2; ++cs)
+    table[(size_t)g * N + pair * 32 + 16 * t + 8 * cs + c] = m[cs] > 0.f ? m[cs] / 127.0f : 1.0f;
+}
+
 // Dynamic LDS of one launch.
 size_t gemv_ktl_pad(int SK, int ktw) { return (size_t)SK * ((((ktw + 3) >> 2) + SK - 1) / SK) * 4; }
 size_t gemv_lds(int MT, int NPW, int SK, bool alds, int ktw, int M) {
@@ -483,7 +538,7 @@ constexpr size_t kAldsMax = 48 * 1024;   // A slices up to this many bytes are s
 
 constexpr size_t kXfAldsMax = 96 * 1024;   // the fused transform stages the slice in LDS up to this size
 
-template <int KB, int MT, int NPW, int SK, bool ALDS, int XF>
+template <int KB, int MT, int NPW, int SK, bool ALDS, int XF, bool WQ = false>
 void launch_gemv(const r4d_gemv_args& a) {
   dim3 grid(a.N / 32 / NPW, a.SKG), block(64 * NPW * SK);
   const int ktw = a.K / 16 / a.SKG;
@@ -491,15 +546,16 @@ void launch_gemv(const r4d_gemv_args& a) {
   if (smem > 160 * 1024) r4d::fail("gemm_trellis_nt_m64", "LDS request above 160 KiB");
   static bool attr = false;
   if (!attr && smem > 64 * 1024) {
-    (void)hipFuncSetAttribute((const void*)tq_gemv_kernel<KB, MT, NPW, SK, ALDS, XF>,
+    (void)hipFuncSetAttribute((const void*)tq_gemv_kernel<KB, MT, NPW, SK, ALDS, XF, WQ>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     attr = true;
   }
-  hipLaunchKernelGGL((tq_gemv_kernel<KB, MT, NPW, SK, ALDS, XF>), grid, block, smem, (hipStream_t)a.stream,
+  hipLaunchKernelGGL((tq_gemv_kernel<KB, MT, NPW, SK, ALDS, XF, WQ>), grid, block, smem, (hipStream_t)a.stream,
                      (const unsigned short*)a.a0, (const unsigned short*)(a.a1 ? a.a1 : a.a0), a.n_split,
                      (const unsigned*)a.w, (const float*)a.svh, (void*)a.c, (float*)a.ws,
                      (unsigned*)a.tickets, a.M, a.K, a.N, a.SKG, a.full, a.out_scale, (const float*)a.suh0,
-                     (const float*)(a.suh1 ? a.suh1 : a.suh0), a.xscale, (unsigned long long*)a.clk);
+                     (const float*)(a.suh1 ? a.suh1 : a.suh0), a.xscale, (unsigned long long*)a.clk,
+                     (const float*)a.wsc, a.wq_gsh);
 }
 
 template <int KB, int MT, int NPW, int SK>
@@ -510,6 +566,13 @@ void launch_gemv_a(const r4d_gemv_args& a) {
     if (abytes > kXfAldsMax) r4d::fail("trellis_gemv_xf", "the A slice does not fit LDS: raise SKG");
     if (a.xf == 2) launch_gemv<KB, MT, NPW, SK, true, 2>(a);
     else launch_gemv<KB, MT, NPW, SK, true, 1>(a);
+  } else if (a.wsc) {
+    if constexpr (KB == 4 || KB == 5) {
+      if (abytes <= kAldsMax) launch_gemv<KB, MT, NPW, SK, true, 0, true>(a);
+      else launch_gemv<KB, MT, NPW, SK, false, 0, true>(a);
+    } else {
+      r4d::fail("gemm_trellis_nt_m64_wq", "KB must be 4 or 5");
+    }
   } else if (abytes <= kAldsMax) {
     launch_gemv<KB, MT, NPW, SK, true, 0>(a);
   } else {
@@ -583,6 +646,55 @@ void r4d_gemm_trellis_nt_m64_raw(int64_t a0, int64_t a1, int n_split, int64_t w,
   a.sk1 = SK == 1;
   a.clk = clk;
   tq_run(a, "gemm_trellis_nt_m64_raw");
+}
+
+// r4d.h:425-450: the fake-quant measurement entries -- r4d_gemm_trellis_nt_m64 / _raw with every decoded weight
+// rounded to int8 under its (column, 2^gsh k-tile group) scale before the MFMA; the legality is the entry's own,
+// plus KB 4 or 5, gsh 1..3 with 16 << gsh dividing K, and a non-null table.
+static void wq_check(int K, int KB, int64_t wscale, int gsh, const char* entry) {
+  if (!wscale) r4d::fail(entry, "the _wq entry needs a scale table (r4d_trellis_wscale_f32)");
+  if (gsh < 1 || gsh > 3 || K % (16 << gsh)) r4d::fail(entry, "gsh must be 1, 2 or 3 with 16 << gsh dividing K");
+  if (KB != 4 && KB != 5) r4d::fail(entry, "KB must be 4 or 5");
+}
+void r4d_gemm_trellis_nt_m64_wq(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c, int64_t ws,
+                                int64_t tickets, int M, int K, int N, int KB, int WV, int SK, int MT, int NP, int SKG,
+                                int U, int NT, float out_scale, int64_t wscale, int gsh, int64_t stream) {
+  (void)WV; (void)MT; (void)NP; (void)U; (void)NT;
+  wq_check(K, KB, wscale, gsh, "gemm_trellis_nt_m64_wq");
+  r4d_gemv_args a{a0, a1, n_split, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale, stream};
+  a.sk1 = SK == 1;
+  a.wsc = wscale;
+  a.wq_gsh = gsh;
+  tq_run(a, "gemm_trellis_nt_m64_wq");
+}
+void r4d_gemm_trellis_nt_m64_raw_wq(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t c, int64_t ws,
+                                    int64_t tickets, int M, int K, int N, int KB, int WV, int SK, int MT, int NP,
+                                    int SKG, int U, int NT, int64_t wscale, int gsh, int64_t stream) {
+  (void)WV; (void)MT; (void)NP; (void)U; (void)NT;
+  wq_check(K, KB, wscale, gsh, "gemm_trellis_nt_m64_raw_wq");
+  r4d_gemv_args a{a0, a1, n_split, w, 0, c, ws, tickets, M, K, N, KB, SKG, 0, 1.f, stream};
+  a.sk1 = SK == 1;
+  a.wsc = wscale;
+  a.wq_gsh = gsh;
+  tq_run(a, "gemm_trellis_nt_m64_raw_wq");
+}
+// r4d.h:433-436, 441-442
+size_t r4d_trellis_wscale_count(int K, int N, int gsh) {
+  if (K <= 0 || N <= 0 || gsh < 1 || gsh > 3) return 0;
+  return (size_t)((K / 16) >> gsh) * (size_t)N;
+}
+void r4d_trellis_wscale_f32(int64_t w, int64_t scale, int K, int N, int KB, int gsh, int64_t stream) {
+  const char* e = "trellis_wscale_f32";
+  if (!w || !scale) r4d::fail(e, "null w or scale");
+  if (KB != 4 && KB != 5) r4d::fail(e, "KB must be 4 or 5");
+  if (N <= 0 || N % 32) r4d::fail(e, "N must be a positive multiple of 32");
+  if (gsh < 1 || gsh > 3 || K <= 0 || K % (16 << gsh) || (K / 16) % 4) r4d::fail(e, "gsh 1..3, 16 << gsh and 64 dividing K");
+  const int ktb = (1 << gsh) > 4 ? (1 << gsh) : 4;
+  const long long waves = (long long)(N / 32) * ((K / 16) / ktb);
+  dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  if (KB == 4) hipLaunchKernelGGL(tq_wscale_kernel<4>, grid, block, 0, (hipStream_t)stream, (const unsigned*)w, (float*)scale, K, N, gsh);
+  else hipLaunchKernelGGL(tq_wscale_kernel<5>, grid, block, 0, (hipStream_t)stream, (const unsigned*)w, (float*)scale, K, N, gsh);
+  r4d::launch_ok(e);
 }
 
 // No reference counterpart: the input transform of r4dx_trellis_input_f16 / _bf16 fused into the GEMV.

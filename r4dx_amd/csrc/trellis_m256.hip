@@ -50,11 +50,12 @@ __device__ __forceinline__ int m2_slot(int r, int c) { return (r * 8 + (c ^ m2_s
 // fragment read (16 consecutive columns of one chunk) stays a permutation of 16 bank slots.
 __device__ __forceinline__ int m2_bslot(int n, int c) { return c * 2048 + ((n ^ (((n >> 4) & 1) << 3)) * 16); }
 
-template <int KB, int RT>
+template <int KB, int RT, bool WQ = false>
 __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
     const unsigned short* __restrict__ A0, const unsigned short* __restrict__ A1, int n_split,
     const unsigned* __restrict__ W, const float* __restrict__ svh, void* __restrict__ Cv,
-    float* __restrict__ ws, int M, int K, int N, int SKG, int full, float out_scale) {
+    float* __restrict__ ws, int M, int K, int N, int SKG, int full, float out_scale,
+    const float* __restrict__ wsc, int wq_gsh) {
   constexpr int BLK = 16 * KB;                    // words per (pair, k-tile) block
   constexpr unsigned kStepBytes = 4 * BLK * 4;    // one pair's words per step
   constexpr int MR = 32 * RT;                     // rows of the launch (128 or 256)
@@ -119,6 +120,15 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
       }
       unsigned d[2][2][4];
       r4_decode<KB>(s.w, d);
+      if constexpr (WQ) {
+        // the _wq measurement: the producer rounds its tile pair's weights before publishing them, so every
+        // row group's MFMA sees the same values the M <= 64 _wq kernel feeds its MFMA
+        // (a put past the last step carries the clamped last step's words: use its k-tile, inside the table)
+        const int kt = kt0 + min(st, nst - 1) * 4 + q;
+        const size_t row = (size_t)(kt >> wq_gsh) * N + (size_t)pair * 32 + 16 * t + c;
+        const float sc[2] = {wsc[row], wsc[row + 8]};
+        r4_wq_apply(d, sc);
+      }
 #pragma unroll
       for (int cs = 0; cs < 2; ++cs) {
         const int n = 32 * p + 16 * t + 8 * cs + c;
@@ -363,32 +373,39 @@ std::string m256_check(int M, int K, int N, int n_split, int KB, int SKG) {
   return "";
 }
 
-template <int KB, int RT>
+template <int KB, int RT, bool WQ>
 void m256_launch_rt(const unsigned short* a0, const unsigned short* a1, int n_split, const unsigned* w,
                     const float* svh, void* c, float* ws, int M, int K, int N, int SKG, int full, float out_scale,
-                    hipStream_t st) {
+                    const float* wsc, int wq_gsh, hipStream_t st) {
   constexpr unsigned lds = 2 * (32 * RT * 128 + 128 * 128);
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute((const void*)tq_m256_kernel<KB, RT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    (void)hipFuncSetAttribute((const void*)tq_m256_kernel<KB, RT, WQ>, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)lds);
     attr = true;
   }
-  hipLaunchKernelGGL((tq_m256_kernel<KB, RT>), dim3(N / 128, SKG), dim3(64 * kM2Waves), lds, st, a0, a1, n_split, w,
-                     svh, c, ws, M, K, N, SKG, full, out_scale);
+  hipLaunchKernelGGL((tq_m256_kernel<KB, RT, WQ>), dim3(N / 128, SKG), dim3(64 * kM2Waves), lds, st, a0, a1, n_split,
+                     w, svh, c, ws, M, K, N, SKG, full, out_scale, wsc, wq_gsh);
 }
 template <int KB>
 void m256_launch(int M, const unsigned short* a0, const unsigned short* a1, int n_split, const unsigned* w,
                  const float* svh, void* c, float* ws, unsigned* tickets, int K, int N, int SKG, int full,
-                 float out_scale, hipStream_t st) {
+                 float out_scale, const float* wsc, int wq_gsh, hipStream_t st) {
   (void)tickets;
-  if (M == 256) m256_launch_rt<KB, 8>(a0, a1, n_split, w, svh, c, ws, M, K, N, SKG, full, out_scale, st);
-  else m256_launch_rt<KB, 4>(a0, a1, n_split, w, svh, c, ws, M, K, N, SKG, full, out_scale, st);
+  if (wsc) {
+    if constexpr (KB == 4 || KB == 5) {
+      if (M == 256) m256_launch_rt<KB, 8, true>(a0, a1, n_split, w, svh, c, ws, M, K, N, SKG, full, out_scale, wsc, wq_gsh, st);
+      else m256_launch_rt<KB, 4, true>(a0, a1, n_split, w, svh, c, ws, M, K, N, SKG, full, out_scale, wsc, wq_gsh, st);
+    }
+    return;
+  }
+  if (M == 256) m256_launch_rt<KB, 8, false>(a0, a1, n_split, w, svh, c, ws, M, K, N, SKG, full, out_scale, nullptr, 0, st);
+  else m256_launch_rt<KB, 4, false>(a0, a1, n_split, w, svh, c, ws, M, K, N, SKG, full, out_scale, nullptr, 0, st);
 }
 
 void m256_run(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c, int64_t ws,
               int64_t tickets, int M, int K, int N, int KB, int SKG, int full, float out_scale, int64_t stream,
-              const char* entry) {
+              const char* entry, int64_t wscale = 0, int wq_gsh = 0) {
   r4d::require(entry, m256_check(M, K, N, n_split, KB, SKG));
   if (!a0 || !w || !c) r4d::fail(entry, "null A, W or C");
   if (full && !svh) r4d::fail(entry, "svh must be non-null");
@@ -399,9 +416,10 @@ void m256_run(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64
   auto WS = (float*)ws;
   auto T = (unsigned*)tickets;
   hipStream_t st = (hipStream_t)stream;
-  if (KB == 4) m256_launch<4>(M, A0, A1, n_split, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, st);
-  else if (KB == 5) m256_launch<5>(M, A0, A1, n_split, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, st);
-  else m256_launch<3>(M, A0, A1, n_split, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, st);
+  auto WSC = (const float*)wscale;
+  if (KB == 4) m256_launch<4>(M, A0, A1, n_split, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st);
+  else if (KB == 5) m256_launch<5>(M, A0, A1, n_split, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st);
+  else m256_launch<3>(M, A0, A1, n_split, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st);
   if (SKG > 1) r4d::launch_split_finish(WS, S, (void*)c, M, N, SKG, full, out_scale, st);
   r4d::launch_ok(entry);
 }
@@ -444,6 +462,22 @@ size_t r4d_gemm_trellis_nt_m256_ws_bytes(int M, int N, int SKG) {
 void r4d_gemm_trellis_nt_m256_raw(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t c, int64_t ws,
                                   int64_t tickets, int M, int K, int N, int KB, int SKG, int64_t stream) {
   m256_run(a0, a1, n_split, w, 0, c, ws, tickets, M, K, N, KB, SKG, 0, 1.f, stream, "gemm_trellis_nt_m256_raw");
+}
+
+// r4d.h:451-454: r4d_gemm_trellis_nt_m256 with the weight fake-quant of the _wq entries (the scale table of
+// r4d_trellis_wscale_f32, 2^gsh k-tiles per group; a null table throws). Bit-identical, per element, to
+// r4d_gemm_trellis_nt_m64_wq at M = 64, SK = 1 and the same SKG.
+void r4d_gemm_trellis_nt_m256_wq(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
+                                 int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SK, int NP,
+                                 int SKG, int U, float out_scale, int64_t stream, int skw, int64_t wscale,
+                                 int gsh) {
+  (void)NP; (void)U; (void)skw;
+  const char* e = "gemm_trellis_nt_m256_wq";
+  if (SK != 0 && SK != 1) r4d::fail(e, sk_msg);
+  if (!wscale) r4d::fail(e, "the _wq entry needs a scale table (r4d_trellis_wscale_f32)");
+  if (gsh < 1 || gsh > 3 || K % (16 << gsh)) r4d::fail(e, "gsh must be 1, 2 or 3 with 16 << gsh dividing K");
+  if (KB != 4 && KB != 5) r4d::fail(e, "KB must be 4 or 5");
+  m256_run(a0, a1, n_split, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale, stream, e, wscale, gsh);
 }
 
 // This build's K split for the prefill GEMM: the workgroup count per CU decides the critical path

@@ -65,6 +65,11 @@ SIGS = {
     "r4dx_trellis_input_bf16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
     "r4dx_trellis_input_f16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
     "r4dx_fwht128_f32": (None, [I64, I64, I32, I64]),
+    "r4d_trellis_wscale_count": (SZ, [I32, I32, I32]),
+    "r4d_trellis_wscale_f32": (None, [I64, I64, I32, I32, I32, I32, I64]),
+    "r4d_gemm_trellis_nt_m64_wq": (None, [I64, I64, I32, I64, I64, I64, I64, I64] + [I32] * 11 + [F32, I64, I32, I64]),
+    "r4d_gemm_trellis_nt_m64_raw_wq": (None, [I64, I64, I32, I64, I64, I64, I64] + [I32] * 11 + [I64, I32, I64]),
+    "r4d_gemm_trellis_nt_m256_wq": (None, [I64, I64, I32, I64, I64, I64, I64, I64] + [I32] * 8 + [F32, I64, I32, I64, I32]),
     "r4dx_silu_mul_trellis_bf16": (None, [I64] * 6 + [I32, I64]),
     "r4dx_attn_gate_mul_trellis_bf16": (None, [I64] * 6 + [I32, I64]),
     "r4dx_silu_mul_trellis_i8": (None, [I64] * 7 + [I32, I64]),

@@ -63,6 +63,8 @@ _SIGS = {
     "r4o_w4_dequant": (None, [P, P, I32, I32, I32, P]),
     "r4o_w4_gemm_ref": (None, [P, P, P, I32, I32, I32, I32, P, I32]),
     "r4o_argmax_f32": (C.c_int32, [P, I64, P]),
+    "r4o_wq_table": (None, [P, I64, I64, I32, P]),
+    "r4o_wq_apply": (None, [P, I64, I64, I32, P, P]),
     "r4o_now_seconds": (C.c_double, []),
     "r4o_max_threads": (I32, []),
 }
@@ -88,6 +90,8 @@ _REF_SIGS = {
     "ref_i8_rs_half": (C.c_uint16, [C.c_float]),
     "ref_w4_quantize_pack": (None, [P, I32, I32, I32, P, P]),
     "ref_argmax": (C.c_int32, [P, I64, P]),
+    "ref_wq_table": (None, [P, I64, I64, I32, P]),
+    "ref_wq_apply": (None, [P, I64, I64, I32, P, P]),
     "ref_f32_to_f16": (C.c_uint16, [C.c_float]),
     "ref_f32_to_bf16": (C.c_uint16, [C.c_float]),
 }
@@ -168,6 +172,24 @@ def epilogue_from_raw(s, svh, out_scale):
     lib().r4o_epilogue_from_raw(ptr(np.ascontiguousarray(s, np.float32)), M, N,
                                 ptr(np.ascontiguousarray(svh, np.float32)), out_scale, ptr(c))
     return c
+
+
+def wq_table(q, group):
+    """src/model/fake_quant_w.h:118-128: scale table [K/group][N] of Q (f16 bits [K][N])."""
+    K, N = q.shape
+    t = np.empty((K // group, N), np.float32)
+    lib().r4o_wq_table(ptr(np.ascontiguousarray(q, np.uint16)), K, N, group, ptr(t))
+    return t
+
+
+def wq_apply(q, group, t=None):
+    """src/model/fake_quant_w.h:130-138 then f16: the rounded weight Q' (f16 bits [K][N])."""
+    K, N = q.shape
+    q = np.ascontiguousarray(q, np.uint16)
+    t = wq_table(q, group) if t is None else np.ascontiguousarray(t, np.float32)
+    out = np.empty((K, N), np.uint16)
+    lib().r4o_wq_apply(ptr(q), K, N, group, ptr(t), ptr(out))
+    return out
 
 
 def f16_bits_to_f32(b):

@@ -1,10 +1,13 @@
 """CPU checks of the drop-in boundary: libr4d_mi355x.so loads without a GPU, exports every symbol
 include/r4d_mi355x.h declares, and its host-side legality rules answer without launching."""
 import ctypes as C
+import os
 
 import pytest
 
 from r4dx_amd import loader
+
+ROOT = os.path.dirname(loader.PKG)
 
 
 @pytest.fixture(scope="module")
@@ -67,3 +70,22 @@ def test_w4a16_checks(L):
     assert ck(64, 64, 5120, 248320) is None            # A is staged in K chunks: any M up to 64
     assert [L.r4d_gemm_w4a16_nt_m64_has_group(g) for g in (16, 32, 64, 128)] == [0, 1, 1, 0]
     assert L.r4d_gemm_w4a16_nt_m64_group() == 64 and L.r4d_gemm_w4a16_nt_m64_max_m() == 64
+
+
+def test_wq_guards_throw():
+    """r4d.h:446-448: a null table or a bad group shift throws (std::runtime_error naming the rule) before any GPU
+    work; run in a child process, since an exception cannot cross ctypes. The entries are reached with null
+    device pointers, so nothing but the guard can run."""
+    import subprocess
+    import sys
+    calls = [
+        "L.r4d_gemm_trellis_nt_m64_wq(0, 0, 256, 0, 0, 0, 0, 0, 1, 1024, 256, 4, 0, 0, 0, 0, 1, 0, 0, 1.0, 0, 3, 0)",
+        "L.r4d_gemm_trellis_nt_m64_raw_wq(0, 0, 256, 0, 0, 0, 0, 1, 1024, 256, 4, 0, 0, 0, 0, 1, 0, 0, 8, 4, 0)",
+        "L.r4d_gemm_trellis_nt_m256_wq(0, 0, 256, 0, 0, 0, 0, 0, 256, 1024, 256, 4, 0, 0, 1, 0, 1.0, 0, 0, 0, 3)",
+        "L.r4d_trellis_wscale_f32(8, 8, 1024, 256, 3, 3, 0)",
+    ]
+    rules = ["scale table", "gsh must be", "scale table", "KB must be"]
+    for call, rule in zip(calls, rules):
+        code = f"from r4dx_amd.loader import lib; L = lib(); {call}"
+        p = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, cwd=ROOT, timeout=60)
+        assert p.returncode != 0 and rule in p.stderr, (call, p.stderr[-400:])

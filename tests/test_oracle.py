@@ -312,3 +312,59 @@ def test_producers_match_float64(olib):
     refg = O.bf16_bits_to_f32(a).astype(np.float64) / (1.0 + np.exp(-O.bf16_bits_to_f32(gg).astype(np.float64)))
     gotg = O.bf16_bits_to_f32(outg).astype(np.float64)
     assert np.all(np.abs(gotg - refg) <= np.abs(refg) * 2.0**-7 + 1e-30)
+
+
+# ---- weight fake-quant: closed forms (src/model/fake_quant_w.h:96-140) ----------------------------------------
+def _f16(x):
+    return np.asarray(x, np.float16).view(np.uint16)
+
+
+def test_wq_zero_group_and_grid_fixed_points():
+    """An all-zero group takes scale 1 and stays zero; a group already on the int8 grid j / 16 with max 127 / 16
+    has s = 1/16 exactly and every value is a fixed point (a dropped 1 / s or a wrong clamp moves them)."""
+    K, N = 64, 4
+    q = np.zeros((K, N), np.float32)
+    j = np.arange(-127, 128)
+    rng = np.random.default_rng(5)
+    q[:, 1] = rng.choice(j, K) / 16.0
+    q[7, 1] = 127 / 16.0
+    q[:32, 2] = rng.choice(j, 32) / 16.0
+    q[3, 2] = -127 / 16.0
+    q[32:, 2] = rng.choice(j, 32) * 2.0 ** -8
+    q[40, 2] = 127 * 2.0 ** -8
+    bits = _f16(q)
+    t = O.wq_table(bits, 32)
+    assert t[0, 0] == 1.0 and t[1, 0] == 1.0
+    assert t[0, 2] == np.float32(1 / 16) and t[1, 2] == np.float32(2.0 ** -8)
+    out = O.wq_apply(bits, 32, t)
+    assert np.array_equal(out[:, 0], bits[:, 0])
+    assert np.array_equal(out[:, 2], bits[:, 2])
+    t64 = O.wq_table(bits, 64)
+    assert t64[0, 1] == np.float32(1 / 16)
+    assert np.array_equal(O.wq_apply(bits, 64, t64)[:, 1], bits[:, 1])
+
+
+def test_wq_ties_to_even_and_error_bound():
+    """s = 1 (group max 127): halves go to the even integer (0.5 -> 0, 1.5 -> 2, 2.5 -> 2, -3.5 -> -4); on random
+    decoded weights every value moves by at most s / 2 plus one f16 rounding and lands on the int8 grid."""
+    col = np.zeros(32, np.float32)
+    col[:6] = [127.0, 0.5, 1.5, 2.5, -3.5, -0.5]
+    bits = _f16(col[:, None])
+    out = O.f16_bits_to_f32(O.wq_apply(bits, 32))[:, 0]
+    assert list(out[:6]) == [127.0, 0.0, 2.0, 2.0, -4.0, -0.0]
+    rng = np.random.default_rng(6)
+    K, N, KB = 256, 128, 4
+    words = rng.integers(0, 2**32, K * N * KB // 32, dtype=np.uint64).astype(np.uint32)
+    q = O.decode_pair_grid(words, K, N, KB)
+    for g in (32, 64, 128):
+        t = O.wq_table(q, g)
+        qf = O.f16_bits_to_f32(q).astype(np.float64)
+        amax = np.abs(qf).reshape(K // g, g, N).max(axis=1)
+        assert np.allclose(t, amax / 127, rtol=2 ** -23, atol=0)
+        o = O.f16_bits_to_f32(O.wq_apply(q, g, t)).astype(np.float64)
+        s = np.repeat(t.astype(np.float64), g, axis=0)
+        assert np.all(np.abs(o - qf) <= s / 2 + np.abs(o) * 2.0 ** -11 + 1e-30)
+        # int8 grid: o / s within an f16 rounding of an integer in [-127, 127]
+        r = o / s
+        assert np.all(np.abs(r) <= 127 * (1 + 2.0 ** -10))
+        assert np.all(np.abs(r - np.rint(r)) <= 127 * 2.0 ** -10)

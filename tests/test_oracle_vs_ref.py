@@ -131,3 +131,24 @@ def test_w4a16_and_argmax(olib, rlib):
     for f in rng.standard_normal(2000).astype(np.float32) * 1e3:
         assert olib.r4o_f32_to_f16(f) == rlib.ref_f32_to_f16(f)
         assert olib.r4o_f32_to_bf16(f) == rlib.ref_f32_to_bf16(f)
+
+
+def test_weight_fake_quant(olib, rlib):
+    """r4o_wq_table / r4o_wq_apply against src/model/fake_quant_w.h's FakeQuantWTableRef / FakeQuantWApplyRef
+    (the reference's fp32 product rounded to f16 here, as its kernels do), on decoded trellis weights with an
+    all-zero group planted, at the 32-k and 128-k group widths."""
+    rng = np.random.default_rng(11)
+    for KB, K, N in [(4, 256, 128), (5, 384, 64)]:
+        words = rng.integers(0, 2**32, K * N * KB // 32, dtype=np.uint64).astype(np.uint32)
+        q = O.decode_pair_grid(words, K, N, KB)
+        q[32:64, 5] = 0
+        for group in (32, 128):
+            t = O.wq_table(q, group)
+            tr = np.empty_like(t)
+            rlib.ref_wq_table(ptr(q), K, N, group, ptr(tr))
+            assert np.array_equal(t.view(np.uint32), tr.view(np.uint32))
+            got = O.wq_apply(q, group, t)
+            pr = np.empty((K, N), np.float32)
+            rlib.ref_wq_apply(ptr(q), K, N, group, ptr(t), ptr(pr))
+            want = np.array([rlib.ref_f32_to_f16(float(v)) for v in pr.ravel()], np.uint16).reshape(K, N)
+            assert np.array_equal(got, want)
