@@ -229,6 +229,64 @@ def load_trellis_linear(path, base, spec=None, header=None):
                          L.prescale_log2)
 
 
+COLUMN_PARALLEL, ROW_PARALLEL = "col", "row"
+
+
+def rank_slice(lin, rank, tp, kind, segments=None):
+    """One tensor-parallel rank's share of a trellis linear, as the reference's shard loader cuts it
+    (docs/trellis-kernel.md:187-203, the w4a16 rules of tp_shard.cpp:55-101,259-284):
+      column-parallel (gate_up, qkv, z, q, k, v): every output segment split into tp equal runs of rows; the
+        words of a run are the contiguous pair rows [n0/32, (n0 + cnt)/32) of the pair grid, svh the same rows,
+        suh replicated (all parts, full K); the rank's rows are the segments' runs in order. The segments default
+        to the linear's parts; a fused one-input linear names its own (qkv: q, k, v), and every part boundary
+        must be a segment boundary, so each rank part is the runs of its part's segments;
+      row-parallel (down, o, out_proj): K split into tp equal ranges [k0, k0 + kc); per pair row the k-tiles
+        [k0/16, (k0 + kc)/16) (N/32 runs of kc/16 * 16 KB words), suh cut to the range, svh replicated. The rank's
+        output is the linear's output transform of its partial sum (the transform is linear), so the ranks'
+        outputs add up to the full output.
+    Every range must be 128-aligned (both Hadamards and the scale vectors work in 128-blocks); one GPU runs a
+    rank's share with the same kernels, whatever the rank."""
+    if tp < 1 or not 0 <= rank < tp:
+        raise ValueError(f"rank {rank} of tp {tp}")
+    KT = lin.K // 16
+    tile = 16 * lin.KB                                     # words per (pair, k-tile)
+    grid = lin.words.reshape(lin.N // 32, KT, tile)
+    if kind == COLUMN_PARALLEL:
+        part_rows = list(lin.parts) if lin.parts else [lin.N]
+        segs = part_rows if segments is None else list(segments)
+        bounds = set(np.cumsum(segs).tolist())
+        if sum(segs) != lin.N or not set(np.cumsum(part_rows).tolist()) <= bounds:
+            raise ValueError(f"{lin.base}: segments {segs} must add up to N = {lin.N} and refine the parts")
+        runs, parts, n0, pend, acc = [], [], 0, iter(np.cumsum(part_rows).tolist()), 0
+        pe = next(pend)
+        for seg in segs:
+            cnt = seg // tp
+            if seg % tp or cnt % TRELLIS_BLOCK:
+                raise ValueError(f"{lin.base}: segment {seg} does not split into {tp} 128-aligned runs")
+            runs.append((n0 + rank * cnt, cnt))
+            acc += cnt
+            n0 += seg
+            if n0 == pe:
+                parts.append(acc)
+                acc = 0
+                pe = next(pend, None)
+        words = np.concatenate([grid[a // 32:(a + c) // 32].ravel() for a, c in runs])
+        svh = np.concatenate([lin.svh[a:a + c] for a, c in runs])
+        return TrellisLinear(f"{lin.base}[col {rank}/{tp}]", words, [u.copy() for u in lin.suh], svh, lin.K,
+                             sum(parts), lin.KB, parts if len(parts) > 1 else [], lin.prescale_log2)
+    if kind == ROW_PARALLEL:
+        if len(lin.suh) != 1:
+            raise ValueError(f"{lin.base}: a row-parallel linear has one input part")
+        kc = lin.K // tp
+        if lin.K % tp or kc % TRELLIS_BLOCK:
+            raise ValueError(f"{lin.base}: K = {lin.K} does not split into {tp} 128-aligned ranges")
+        k0 = rank * kc
+        words = np.ascontiguousarray(grid[:, k0 // 16:(k0 + kc) // 16]).ravel()
+        return TrellisLinear(f"{lin.base}[row {rank}/{tp}]", words, [lin.suh[0][k0:k0 + kc].copy()],
+                             lin.svh.copy(), kc, lin.N, lin.KB, list(lin.parts), lin.prescale_log2)
+    raise ValueError(f"kind must be {COLUMN_PARALLEL!r} or {ROW_PARALLEL!r}")
+
+
 def write_container(path, metadata, tensors):
     """A safetensors-shaped file with U8 tensors (name -> uint8 array) and nested-JSON metadata -- the writer half,
     for tests and tools (docs/container-format.md:6-27)."""

@@ -86,12 +86,16 @@ def plan_trellis_i8(N, K, kb, parts=1, part_n0=None, coarse=False):
     why = _shape_why(N, K, kb, parts, part_n0 or 0, rates=(4, 5))
     if why:
         return Plan(False, why)
-    skg = int(lib().r4d_mi355x_i8_skg(K, N))
     n_split = part_n0 if parts == 2 else N
     first = ""
-    for skw in (2, 4, 8):
-        msg = lib().r4d_gemm_trellis_nt_i8_check(PREFILL_M, K, N, n_split, kb, skw, skg)
-        if not msg:
-            return Plan(True, "", "i8c" if coarse else "i8", 0, skg, skw)
-        first = first or msg.decode()
+    # the library's skg first, then smaller splits: (K / 128) must hold skw * skg, and a rank K such as 8704
+    # (68 blocks = 4 * 17) takes skg 4 alone but no skw >= 2 beside it
+    skg = int(lib().r4d_mi355x_i8_skg(K, N))
+    while skg >= 1:
+        for skw in (2, 4, 8):
+            msg = lib().r4d_gemm_trellis_nt_i8_check(PREFILL_M, K, N, n_split, kb, skw, skg)
+            if not msg:
+                return Plan(True, "", "i8c" if coarse else "i8", 0, skg, skw)
+            first = first or msg.decode()
+        skg //= 2
     return Plan(False, first)

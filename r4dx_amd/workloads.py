@@ -18,6 +18,22 @@ LAYER_SHAPES = [
 ]
 
 
+# Tensor-parallel kinds of those projections (docs/trellis-kernel.md:191-203): column-parallel linears split every
+# output segment (gdn.qkv's q, k, v segments; mlp.gate | mlp.up's two parts), row-parallel ones split K. At TP = 2
+# every rank range is 128-aligned; one GPU runs one rank's share.
+TP_KINDS = {
+    "gdn.qkv": ("col", [2048, 2048, 6144]),
+    "gdn.z": ("col", None),
+    "gdn.out": ("row", None),
+    "attn.q": ("col", None),
+    "attn.k": ("col", None),
+    "attn.v": ("col", None),
+    "attn.o": ("row", None),
+    "mlp.gate_up": ("col", [17408, 17408]),
+    "mlp.down": ("row", None),
+}
+
+
 # The engine's launch groups for those projections: (input group, linears); a linear with two names is a
 # fused two-part linear (part 1 from the first part's N on, reading its own input transform).
 LAYER_GROUPS = [

@@ -41,3 +41,21 @@ def test_two_part_plans():
 def test_refusals_name_the_rule(f, args, why):
     p = f(*args)
     assert not p.ok and why in p.why
+
+
+TP2_SHAPES = [(8704 * 2, 5120, 2, 8704), (5120, 5120, 1, None), (3072, 5120, 1, None), (512, 5120, 1, None),
+              (5120, 8704, 1, None), (5120, 3072, 1, None)]
+
+
+@pytest.mark.parametrize("N,K,parts,n0", TP2_SHAPES)
+@pytest.mark.parametrize("kb", [4, 5])
+def test_plans_of_the_tp2_rank_shapes(N, K, parts, n0, kb):
+    """One TP = 2 rank's shapes (docs/trellis-kernel.md:197-203, rank K 8704 = 544 k-tiles = 2^5 17): every planner
+    accepts them and every plan is legal by the kernels' own checks."""
+    decode = [plan.linear_tuning(N, K, kb, M, parts=parts, part_n0=n0) for M in (1, 8, 16)]
+    assert all(p.ok for p in decode) and len({(p.SK, p.SKG) for p in decode}) == 1
+    assert (K // 16) % decode[0].SKG == 0
+    m256 = plan.plan_trellis_m256(N, K, kb, parts=parts, part_n0=n0)
+    assert m256.ok and (K // 16) % m256.SKG == 0
+    i8 = plan.plan_trellis_i8(N, K, kb, parts=parts, part_n0=n0)
+    assert i8.ok

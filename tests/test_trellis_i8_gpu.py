@@ -109,7 +109,7 @@ def test_tables_and_dump_bit_exact(coarse, KB):
 
 CASES = [  # (K, N, KB, skg)
     (512, 384, 4, 1), (1024, 256, 5, 2), (1024, 384, 4, 4), (5120, 17408, 4, 1), (17408, 5120, 4, 4),
-    (5120, 17408, 5, 2), (17408, 5120, 5, 4),
+    (5120, 17408, 5, 2), (17408, 5120, 5, 4), (8704, 5120, 4, 2),  # the last: a TP = 2 rank of mlp.down
 ]
 
 
