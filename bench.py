@@ -96,7 +96,28 @@ def main():
                             tickets=api.TicketBuffer(N, dev).t,
                             out=torch.empty((M, N), dtype=torch.bfloat16, device=dev)))
         groups.append(g)
+        g["lin"] = lin[len(lin) - len(members):]
     out_scale = float(np.float32(1.0 / np.sqrt(128.0)))
+
+    # The same layer with the projections that share an input laid out as one linear (gdn qkv | z, attn q | k | v:
+    # pair grids, svh and outputs concatenated along N), one r4dx_gemm_trellis_nt_m64_parts launch per input
+    # group: 6 GEMV launches instead of 9, the same weights and the same columns.
+    merged = []
+    for g in groups:
+        ms = g["lin"]
+        if len(ms) == 1:
+            merged.append(ms[0])
+            continue
+        K = ms[0]["K"]
+        N = sum(L["N"] for L in ms)
+        skg = api.trellis_gemv_skg(K, N, KB)
+        merged.append(dict(name="|".join(L["name"] for L in ms), K=K, N=N, parts=[L["a"][0] for L in ms],
+                           n0=[int(v) for v in np.cumsum([0] + [L["N"] for L in ms[:-1]])],
+                           words=[torch.cat([L["words"][c] for L in ms]) for c in range(copies)],
+                           svh=torch.cat([L["svh"] for L in ms]), skg=skg,
+                           ws=torch.empty(max(1, skg * M * N), dtype=torch.float32, device=dev),
+                           tickets=api.TicketBuffer(N, dev).t,
+                           out=torch.empty((M, N), dtype=torch.bfloat16, device=dev)))
 
     # Launches go to the current stream (the capture stream while a graph is being captured). The step is the
     # engine's launches for the layer: 6 input transforms and 9 GEMVs; the fused entry (r4dx_trellis_gemv_xf:
@@ -118,6 +139,24 @@ def main():
         for L in lin:
             gemv(L, c)
 
+    def nparts(L):
+        return len(L["parts"]) if "parts" in L else len(L["a"])
+
+    def launch(L, c):
+        if "parts" in L:
+            api.trellis_gemm_m64_parts(L["parts"], L["n0"], L["words"][c], L["svh"], L["K"], L["N"], KB,
+                                       skg=L["skg"], out=L["out"], ws=L["ws"], tickets=L["tickets"],
+                                       out_scale=out_scale)
+        else:
+            gemv(L, c)
+
+    def step_merged(c, gemv_only=False):
+        if not gemv_only:
+            for g in groups:
+                api.trellis_input(g["x"], g["suh"], 0, bf16=False, outs=g["outs"])
+        for L in merged:
+            launch(L, c)
+
     def step_fused(c):
         for L in lin:
             gemv_xf(L, c)
@@ -127,6 +166,7 @@ def main():
     for c in range(copies):   # eager once: A is valid, tickets settle
         step_fused(c)
         step(c)
+        step_merged(c)
     torch.cuda.synchronize()
     if args.pmc:
         # calibration: a plain device copy of a known size (the counters' bytes per algorithmic byte)
@@ -137,11 +177,11 @@ def main():
         torch.cuda.synchronize()
         for _ in range(2):
             for c in range(copies):
-                for L in lin:
-                    gemv(L, c)
+                for L in merged:
+                    launch(L, c)
         torch.cuda.synchronize()
         print(json.dumps({"pmc_pass": "done", "copy_bytes": 512 << 20, "launch_order": [
-            [L["name"], L["K"], L["N"], len(L["a"])] for L in lin]}), flush=True)
+            [L["name"], L["K"], L["N"], nparts(L)] for L in merged]}), flush=True)
         return
 
     def capture(fn):
@@ -154,7 +194,7 @@ def main():
         torch.cuda.synchronize()
         return g
 
-    g_step = capture(lambda: [step(c, args.kernel_only) for c in range(copies)])
+    g_step = capture(lambda: [step_merged(c, args.kernel_only) for c in range(copies)])
     reps = max(1, -(-args.steps // copies))
     steps = reps * copies
     for _ in range(max(1, -(-args.warmup // copies))):
@@ -178,13 +218,25 @@ def main():
     u1.record(stream)
     torch.cuda.synchronize()
     ms_step_fused = u0.elapsed_time(u1) / copies
+    # the reference engine's launch pattern: one GEMV per projection (9 launches)
+    g_proj = capture(lambda: [step(c) for c in range(copies)])
+    g_proj.replay()
+    v0, v1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    v0.record(stream)
+    for _ in range(reps):
+        g_proj.replay()
+    v1.record(stream)
+    torch.cuda.synchronize()
+    ms_step_proj = v0.elapsed_time(v1) / steps
 
-    # The dominant kernel alone: per shape, a graph of back-to-back launches over the rotating copies.
+    # The dominant kernel alone: per launch shape of the step, a graph of back-to-back launches over the
+    # rotating copies; the per-projection launches beside it.
     R = 4
     gemv_ms, alg_bytes = 0.0, 0.0
-    per_shape = {}
-    for L in lin:
-        g = capture(lambda: [gemv(L, c) for _ in range(R) for c in range(copies)])
+    per_shape, per_proj = {}, {}
+    mids, lids = {id(L) for L in merged}, {id(L) for L in lin}
+    for L in merged + [L for L in lin if id(L) not in mids]:
+        g = capture(lambda: [launch(L, c) for _ in range(R) for c in range(copies)])
         g.replay()
         b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         b0.record(stream)
@@ -193,10 +245,14 @@ def main():
         torch.cuda.synchronize()
         avg_ms = b0.elapsed_time(b1) / (R * copies)
         K, N = L["K"], L["N"]
-        ab = K * N * KB / 8 + len(L["a"]) * M * K * 2 + M * N * 2 + 4 * N
-        gemv_ms += avg_ms
-        alg_bytes += ab
-        per_shape[L["name"]] = {"us": round(avg_ms * 1e3, 2), "GBs": round(ab / (avg_ms * 1e-3) / 1e9, 1)}
+        ab = K * N * KB / 8 + nparts(L) * M * K * 2 + M * N * 2 + 4 * N
+        rec = {"us": round(avg_ms * 1e3, 2), "GBs": round(ab / (avg_ms * 1e-3) / 1e9, 1)}
+        if id(L) in mids:
+            gemv_ms += avg_ms
+            alg_bytes += ab
+            per_shape[L["name"]] = rec
+        if id(L) in lids:
+            per_proj[L["name"]] = rec
     achieved = alg_bytes / (gemv_ms * 1e-3) / 1e9
 
     m256 = None if args.no_m256 else bench_m256(api, WL, KB)
@@ -222,17 +278,24 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (uniform random trellis words, +-1 Hadamard signs, log-normal svh, N(0,1) x)",
-        "config": {"workload": f"config1: the 10 projections of one 27B-class layer as the engine launches them "
-                               f"(9 GEMVs: mlp.gate+up fused), M={M}, KB={KB}, "
+        "config": {"workload": f"config1: the 10 projections of one 27B-class layer, the projections that share an "
+                               f"input laid out as one linear (gdn qkv|z, attn q|k|v, mlp gate|up: 6 GEMV launches, "
+                               f"r4dx_gemm_trellis_nt_m64_parts / r4d_gemm_trellis_nt_m64), M={M}, KB={KB}, "
                                f"{copies} rotating weight copies ({copies * layer_wbytes / 2**30:.2f} GiB)",
                    "M": M, "KB": KB, "weight_bytes_per_step": layer_wbytes,
-                   "step": "6 input transforms (shared by projections with the same input, nout 1-3) + 9 trellis "
-                           "GEMVs (FWHT/svh epilogue, bf16 out)",
+                   "step": "6 input transforms (shared by projections with the same input, nout 1-3) + 6 trellis "
+                           "GEMV launches (FWHT/svh epilogue, bf16 out); every weight byte of the layer read once",
+                   "per_projection_ms_per_step": round(ms_step_proj, 4),
+                   "per_projection_GBs": round(layer_wbytes / (ms_step_proj * 1e-3) / 1e9, 1),
+                   "per_projection_step": "the reference engine's launch pattern: 6 transforms + 9 GEMVs, one per "
+                                          "projection (mlp gate+up fused)",
+                   "per_projection_launch_GBs": per_proj,
                    "fused_xf_ms_per_step": round(ms_step_fused, 4),
-                   "fused_xf_GBs": round(layer_wbytes / (ms_step_fused * 1e-3) / 1e9, 1)},
+                   "fused_xf_GBs": round(layer_wbytes / (ms_step_fused * 1e-3) / 1e9, 1),
+                   "fused_xf_step": "9 r4dx_trellis_gemv_xf launches (transform inside the GEMV), per projection"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic("tq_gemv_kernel", KB, M),
-                     "kernel": "tq_gemv_kernel", "avg_launch_us": round(gemv_ms * 1e3 / len(lin), 3),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic("tq_gemv_kernel", KB, M, [L["name"] for L in merged]),
+                     "kernel": "tq_gemv_kernel", "avg_launch_us": round(gemv_ms * 1e3 / len(merged), 3),
                      "per_shape_GBs": per_shape},
         "cpu_baseline": cpu,
         "m256": m256,
@@ -387,9 +450,9 @@ def bench_w4a16(api, WL, R=4):
             "peak_GBs": HBM_PEAK_GBS, "cases": res}
 
 
-def _traffic(kernel, KB, M):
-    """HBM bytes per launch of `kernel` (mean over the config-1 shapes), from the committed summary of the
-    two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE), each scaled by the same counter's reading for a
+def _traffic(kernel, KB, M, names):
+    """HBM bytes per launch of `kernel` (mean over the step's launch shapes `names`), from the committed summary
+    of the two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE), each scaled by the same counter's reading for a
     copy of known size; None when no summary matches this configuration."""
     path = os.path.join(ROOT, "profiles", "gemv_traffic_config1.json")
     try:
@@ -397,7 +460,7 @@ def _traffic(kernel, KB, M):
             t = json.load(f)
     except (OSError, ValueError):
         return None
-    if t.get("kernel") != kernel or t.get("KB") != KB or t.get("M") != M:
+    if t.get("kernel") != kernel or t.get("KB") != KB or t.get("M") != M or set(t.get("per_shape", {})) != set(names):
         return None
     return t.get("hbm_bytes_per_launch")
 

@@ -188,6 +188,16 @@ void r4dx_trellis_input_bf16(int64_t x, int64_t M, int64_t K, int nout, const in
 /* The same for an f16 x (fp16 activations); no reference counterpart, same contract. */
 void r4dx_trellis_input_f16(int64_t x, int64_t M, int64_t K, int nout, const int64_t* suh,
                             const int64_t* out, int prescale_log2, int64_t stream);
+/* No reference counterpart: r4d_gemm_trellis_nt_m64 over up to four input parts. Projections that read one input
+ * (q | k | v, gdn qkv | z) stored as one linear -- their pair grids, svh and outputs concatenated along N -- run as
+ * one launch; columns [n0[p], n0[p + 1]) read a[p] (the transform of the input under that projection's suh). a and
+ * n0 are host arrays of `parts` (1..4) entries, n0[0] = 0, rising in multiples of 128 below N. Every column equals
+ * the one-part launch of its projection at the same SKG, bit for bit. The _check form returns nullptr or the rule. */
+const char* r4dx_gemm_trellis_nt_m64_parts_check(int parts, const int* n0, int M, int K, int N, int KB, int SKG,
+                                                 int have_ws);
+void r4dx_gemm_trellis_nt_m64_parts(const int64_t* a, const int* n0, int parts, int64_t w, int64_t svh, int64_t c,
+                                    int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SKG,
+                                    float out_scale, int64_t stream);
 /* r4d.h:425-454 weight fake-quant, a measurement hook: r4d_gemm_trellis_nt_m64 / _raw / r4d_gemm_trellis_nt_m256
  * with every decoded weight w rounded, right before the MFMA, to f16(clamp(rint(w (1 / s)), -127, 127) s) (all but
  * the last rounding in fp32) under its column's scale s of a group of 2^gsh k-tiles. The table [K / 16 >> gsh][N]

@@ -66,4 +66,8 @@ struct r4d_gemv_args {
   // the _wq measurement entries: the weight scale table [K / 16 >> wq_gsh][N] (0: off) and its group shift
   int64_t wsc;
   int wq_gsh;
+  // more input parts (r4dx_gemm_trellis_nt_m64_parts): columns from n_end1 on read a2, from n_end2 on a3
+  // (0: no such part)
+  int64_t a2, a3;
+  int n_end1, n_end2;
 };

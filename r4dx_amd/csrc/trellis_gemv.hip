@@ -92,9 +92,15 @@ constexpr int kRedRows = 4;          // rows of the final slice sum per pass
 // XF > 0: A0 is the raw input x [M][K] (XF 1: f16, 2: bf16) and the workgroup stages its own slice of the
 // transformed A = f16(FWHT128(fp32(x) * suh) * xscale) (suh0 / suh1 by column part) straight into LDS --
 // the arithmetic of r4dx_trellis_input_*, so A is bit-identical to the unfused path's.
+// The input parts: columns [n_end[p - 1], n_end[p]) read a[p] (n_end[3] is past every column).
+struct R4AParts {
+  const unsigned short* a[4];
+  int n_end[3];
+};
+
 template <int KB, int MT, int NPW, int SK, bool ALDS, int XF, bool WQ = false>
 __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
-    const unsigned short* __restrict__ A0, const unsigned short* __restrict__ A1, int n_split,
+    const R4AParts ap,
     const unsigned* __restrict__ W, const float* __restrict__ svh, void* __restrict__ Cv,
     float* __restrict__ ws, unsigned* __restrict__ tickets, int M, int K, int N, int SKG, int full,
     float out_scale, const float* __restrict__ suh0, const float* __restrict__ suh1, float xscale,
@@ -118,7 +124,11 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
   const int pair = blockIdx.x * NPW + pl;
   const int group = (blockIdx.x * NPW) >> 2;
   const int KT = K >> 4, ktw = KT / SKG, kt0 = ky * ktw;
-  const unsigned short* __restrict__ A = group * 128 >= n_split ? A1 : A0;
+  const unsigned short* __restrict__ A0 = ap.a[0];
+  const int n_split = ap.n_end[0];
+  const unsigned short* __restrict__ A = group * 128 < ap.n_end[0] ? ap.a[0]
+                                       : group * 128 < ap.n_end[1] ? ap.a[1]
+                                       : group * 128 < ap.n_end[2] ? ap.a[2] : ap.a[3];
   const int q = lane >> 4, t = (lane >> 3) & 1, c = lane & 7, mrow = lane & 15;
 
   // Steps (4 k-tiles each) of the slice, split into SK contiguous parts of at most nsw steps.
@@ -550,8 +560,15 @@ void launch_gemv(const r4d_gemv_args& a) {
                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     attr = true;
   }
-  hipLaunchKernelGGL((tq_gemv_kernel<KB, MT, NPW, SK, ALDS, XF, WQ>), grid, block, smem, (hipStream_t)a.stream,
-                     (const unsigned short*)a.a0, (const unsigned short*)(a.a1 ? a.a1 : a.a0), a.n_split,
+  R4AParts ap;
+  ap.a[0] = (const unsigned short*)a.a0;
+  ap.a[1] = (const unsigned short*)(a.a1 ? a.a1 : a.a0);
+  ap.a[2] = a.a2 ? (const unsigned short*)a.a2 : ap.a[1];
+  ap.a[3] = a.a3 ? (const unsigned short*)a.a3 : ap.a[2];
+  ap.n_end[0] = a.n_split;
+  ap.n_end[1] = a.a2 ? a.n_end1 : 0x7FFFFFFF;
+  ap.n_end[2] = a.a3 ? a.n_end2 : 0x7FFFFFFF;
+  hipLaunchKernelGGL((tq_gemv_kernel<KB, MT, NPW, SK, ALDS, XF, WQ>), grid, block, smem, (hipStream_t)a.stream, ap,
                      (const unsigned*)a.w, (const float*)a.svh, (void*)a.c, (float*)a.ws,
                      (unsigned*)a.tickets, a.M, a.K, a.N, a.SKG, a.full, a.out_scale, (const float*)a.suh0,
                      (const float*)(a.suh1 ? a.suh1 : a.suh0), a.xscale, (unsigned long long*)a.clk,
@@ -695,6 +712,39 @@ void r4d_trellis_wscale_f32(int64_t w, int64_t scale, int K, int N, int KB, int 
   if (KB == 4) hipLaunchKernelGGL(tq_wscale_kernel<4>, grid, block, 0, (hipStream_t)stream, (const unsigned*)w, (float*)scale, K, N, gsh);
   else hipLaunchKernelGGL(tq_wscale_kernel<5>, grid, block, 0, (hipStream_t)stream, (const unsigned*)w, (float*)scale, K, N, gsh);
   r4d::launch_ok(e);
+}
+
+// No reference counterpart: r4d_gemm_trellis_nt_m64 over up to four input parts -- the projections that share
+// one input (q | k | v, qkv | z) laid out as one linear whose column ranges read their own transformed input
+// (a[p] for columns [n0[p], n0[p + 1])), one launch instead of one per projection. Columns compute exactly as in
+// the one-part launch of that range at the same SKG.
+const char* r4dx_gemm_trellis_nt_m64_parts_check(int parts, const int* n0, int M, int K, int N, int KB, int SKG,
+                                                 int have_ws) {
+  std::string e;
+  if (parts < 1 || parts > 4 || !n0) e = "parts must be 1..4 with their first columns n0";
+  else if (n0[0] != 0) e = "n0[0] must be 0";
+  else {
+    for (int p = 1; p < parts && e.empty(); ++p)
+      if (n0[p] <= n0[p - 1] || n0[p] >= N || n0[p] % 128) e = "n0 must rise in multiples of 128 below N";
+  }
+  if (!e.empty()) return r4d::check_result(e);
+  return r4d_gemm_trellis_nt_m64_check(M, K, N, parts > 1 ? n0[1] : N, KB, SKG, 1, 1, have_ws);
+}
+
+void r4dx_gemm_trellis_nt_m64_parts(const int64_t* a, const int* n0, int parts, int64_t w, int64_t svh, int64_t c,
+                                    int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SKG,
+                                    float out_scale, int64_t stream) {
+  const char* e = "gemm_trellis_nt_m64_parts";
+  if (!a || !n0) r4d::fail(e, "null part arrays");
+  if (const char* m = r4dx_gemm_trellis_nt_m64_parts_check(parts, n0, M, K, N, KB, SKG, ws != 0 && tickets != 0))
+    r4d::fail(e, m);
+  for (int p = 0; p < parts; ++p)
+    if (!a[p]) r4d::fail(e, "null part input");
+  r4d_gemv_args g{a[0], parts > 1 ? a[1] : 0, parts > 1 ? n0[1] : N, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1,
+                  out_scale, stream};
+  if (parts > 2) { g.a2 = a[2]; g.n_end1 = n0[2]; }
+  if (parts > 3) { g.a3 = a[3]; g.n_end2 = n0[3]; }
+  tq_run(g, e);
 }
 
 // No reference counterpart: the input transform of r4dx_trellis_input_f16 / _bf16 fused into the GEMV.

@@ -10,6 +10,7 @@ HEADER = os.path.join(os.path.dirname(PKG), "include", "r4d_mi355x.h")
 I64, I32, F32, SZ, P = C.c_int64, C.c_int, C.c_float, C.c_size_t, C.c_void_p
 CSTR = C.c_char_p
 I64P = C.POINTER(C.c_int64)
+I32P = C.POINTER(C.c_int)
 
 SIGS = {
     "r4d_gemm_trellis_nt_m64": (None, [I64, I64, I32, I64, I64, I64, I64, I64] + [I32] * 11 + [F32, I64]),
@@ -65,6 +66,8 @@ SIGS = {
     "r4dx_trellis_input_bf16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
     "r4dx_trellis_input_f16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),
     "r4dx_fwht128_f32": (None, [I64, I64, I32, I64]),
+    "r4dx_gemm_trellis_nt_m64_parts_check": (CSTR, [I32, I32P, I32, I32, I32, I32, I32, I32]),
+    "r4dx_gemm_trellis_nt_m64_parts": (None, [I64P, I32P, I32] + [I64] * 5 + [I32] * 5 + [F32, I64]),
     "r4d_trellis_wscale_count": (SZ, [I32, I32, I32]),
     "r4d_trellis_wscale_f32": (None, [I64, I64, I32, I32, I32, I32, I64]),
     "r4d_gemm_trellis_nt_m64_wq": (None, [I64, I64, I32, I64, I64, I64, I64, I64] + [I32] * 11 + [F32, I64, I32, I64]),

@@ -89,3 +89,15 @@ def test_wq_guards_throw():
         code = f"from r4dx_amd.loader import lib; L = lib(); {call}"
         p = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, cwd=ROOT, timeout=60)
         assert p.returncode != 0 and rule in p.stderr, (call, p.stderr[-400:])
+
+
+def test_parts_check(L):
+    def chk(n0, M=1, K=1024, N=1024, KB=4, SKG=1):
+        a = (C.c_int * len(n0))(*n0)
+        return L.r4dx_gemm_trellis_nt_m64_parts_check(len(n0), a, M, K, N, KB, SKG, 1)
+    assert chk([0]) is None and chk([0, 256, 512, 768]) is None
+    assert b"n0[0]" in chk([128, 256])
+    assert b"rise" in chk([0, 512, 256]) and b"rise" in chk([0, 100]) and b"rise" in chk([0, 1024])
+    assert b"parts" in L.r4dx_gemm_trellis_nt_m64_parts_check(5, (C.c_int * 5)(0, 128, 256, 384, 512), 1, 1024,
+                                                              1024, 4, 1, 1)
+    assert b"M must be" in chk([0, 256], M=65)

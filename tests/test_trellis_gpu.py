@@ -205,3 +205,30 @@ def test_gemv_fused_transform_bit_identical(KB, K, N, M, skg, bf16, prescale):
                               prescale=prescale, bf16=bf16, out_scale=0.0883883)
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("M,KB,widths", [(1, 4, (6144, 1024, 1024)), (8, 5, (10240, 6144)),
+                                         (64, 4, (256, 128, 384, 256)), (3, 5, (1024, 512, 512))])
+def test_parts_launch_equals_one_launch_per_projection(M, KB, widths):
+    """r4dx_gemm_trellis_nt_m64_parts: projections that share one input, laid out as one linear, give every column
+    exactly what the projection's own launch gives at the same SKG; and the whole against the fp64 oracle."""
+    banner("parts", M, KB, widths)
+    K = 5120 if widths[0] > 1024 else 1024
+    N = sum(widths)
+    n0 = [int(x) for x in np.concatenate([[0], np.cumsum(widths)[:-1]])]
+    words, _, svh = WL.trellis_linear(K, N, KB, 11 * M + KB)
+    a = [WL.activations_f16(M, K, 70 + p).view(np.uint16) for p in range(len(widths))]
+    a_d = [dev(x) for x in a]
+    skg = api.trellis_gemv_skg(K, N, KB)
+    osc = float(np.float32(1.0 / np.sqrt(128.0)))
+    whole = host_u16(api.trellis_gemm_m64_parts(a_d, n0, dev(words), dev(svh), K, N, KB, skg=skg, out_scale=osc))
+    grid = words.reshape(N // 32, -1)
+    q = O.decode_pair_grid(words, K, N, KB)
+    for p, (c0, wdt) in enumerate(zip(n0, widths)):
+        w_p = np.ascontiguousarray(grid[c0 // 32:(c0 + wdt) // 32]).ravel()
+        one = host_u16(api.trellis_gemm_m64(a_d[p], dev(w_p), dev(svh[c0:c0 + wdt]), K, wdt, KB, skg=skg,
+                                            out_scale=osc))
+        torch.cuda.synchronize()
+        assert np.array_equal(whole[:, c0:c0 + wdt], one), p
+        ref = O.linear_from_a(a[p], np.ascontiguousarray(q[:, c0:c0 + wdt]), svh[c0:c0 + wdt])
+        assert close_rel(O.bf16_bits_to_f32(whole[:, c0:c0 + wdt]), ref, 2.0**-8, 1e-3) <= 1.0
