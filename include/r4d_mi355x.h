@@ -198,6 +198,13 @@ const char* r4dx_gemm_trellis_nt_m64_parts_check(int parts, const int* n0, int M
 void r4dx_gemm_trellis_nt_m64_parts(const int64_t* a, const int* n0, int parts, int64_t w, int64_t svh, int64_t c,
                                     int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SKG,
                                     float out_scale, int64_t stream);
+/* No reference counterpart: the prefill form of the above, r4d_gemm_trellis_nt_m256 (M = 128 or 256) over up to four
+ * input parts with the same a / n0 rule; every column equals the one-part M = 256 launch of its range at the same
+ * SKG. */
+const char* r4dx_gemm_trellis_nt_m256_parts_check(int parts, const int* n0, int M, int K, int N, int KB, int SKG);
+void r4dx_gemm_trellis_nt_m256_parts(const int64_t* a, const int* n0, int parts, int64_t w, int64_t svh, int64_t c,
+                                     int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SKG,
+                                     float out_scale, int64_t stream);
 /* r4d.h:425-454 weight fake-quant, a measurement hook: r4d_gemm_trellis_nt_m64 / _raw / r4d_gemm_trellis_nt_m256
  * with every decoded weight w rounded, right before the MFMA, to f16(clamp(rint(w (1 / s)), -127, 127) s) (all but
  * the last rounding in fp32) under its column's scale s of a group of 2^gsh k-tiles. The table [K / 16 >> gsh][N]

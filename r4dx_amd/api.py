@@ -109,6 +109,30 @@ def trellis_gemm_m64_parts(a_parts, n0, w, svh, K, N, KB, skg=None, out=None, ws
     return out
 
 
+def trellis_gemm_m256_parts(a_parts, n0, w, svh, K, N, KB, skg=None, out=None, ws=None, tickets=None,
+                            out_scale=1.0, stream=None):
+    """r4dx_gemm_trellis_nt_m256_parts: the M = 128 / 256 GEMM of one linear whose columns [n0[p], n0[p + 1]) read
+    a_parts[p] (bf16 [M][N])."""
+    L = lib()
+    M = a_parts[0].shape[0]
+    parts = len(a_parts)
+    skg = trellis_m256_skg(K, N, KB) if skg is None else skg
+    n0a = (C.c_int * parts)(*n0)
+    msg = L.r4dx_gemm_trellis_nt_m256_parts_check(parts, n0a, M, K, N, KB, skg)
+    if msg:
+        raise ValueError(msg.decode())
+    if any(a.shape != (M, K) for a in a_parts) or svh is None:
+        raise ValueError("every part input is [M][K]; svh is required")
+    if ws is None and skg > 1:
+        ws = torch.empty(L.r4d_gemm_trellis_nt_m256_ws_bytes(M, N, skg) // 4, dtype=torch.float32, device=w.device)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=w.device)
+    pa = (C.c_int64 * parts)(*[a.data_ptr() for a in a_parts])
+    L.r4dx_gemm_trellis_nt_m256_parts(pa, n0a, parts, _p(w), _p(svh), _p(out), _p(ws), _p(tickets), M, K, N, KB, skg,
+                                      float(out_scale), _stream(stream))
+    return out
+
+
 def trellis_m256_skg(K, N, KB):
     return lib().r4d_mi355x_trellis_m256_skg(K, N, KB)
 

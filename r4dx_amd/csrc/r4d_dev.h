@@ -34,6 +34,29 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// The input parts of a trellis linear: columns [n_end[p - 1], n_end[p]) read a[p] (n_end[3] is past every
+// column). One part: every n_end past N; the reference's two-part form: n_end[0] = n_split.
+struct R4AParts {
+  const unsigned short* a[4];
+  int n_end[3];
+};
+inline R4AParts r4_parts(const void* a0, const void* a1, int n_split, const void* a2 = nullptr, int n_end1 = 0,
+                         const void* a3 = nullptr, int n_end2 = 0) {
+  R4AParts ap;
+  ap.a[0] = (const unsigned short*)a0;
+  ap.a[1] = a1 ? (const unsigned short*)a1 : ap.a[0];
+  ap.a[2] = a2 ? (const unsigned short*)a2 : ap.a[1];
+  ap.a[3] = a3 ? (const unsigned short*)a3 : ap.a[2];
+  ap.n_end[0] = n_split;
+  ap.n_end[1] = a2 ? n_end1 : 0x7FFFFFFF;
+  ap.n_end[2] = a3 ? n_end2 : 0x7FFFFFFF;
+  return ap;
+}
+// the input of the 128-column group starting at column n0 (uniform per workgroup: scalar compares)
+__device__ __forceinline__ const unsigned short* r4_part_a(const R4AParts& ap, int n0) {
+  return n0 < ap.n_end[0] ? ap.a[0] : n0 < ap.n_end[1] ? ap.a[1] : n0 < ap.n_end[2] ? ap.a[2] : ap.a[3];
+}
+
 typedef _Float16 r4h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 r4h2 __attribute__((ext_vector_type(2)));
 typedef float r4f4 __attribute__((ext_vector_type(4)));

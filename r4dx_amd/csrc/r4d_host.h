@@ -46,6 +46,17 @@ void launch_split_finish(const float* ws, const float* svh, void* c, int M, int 
 }  // namespace r4d
 
 // Arguments of one trellis GEMV launch (trellis_gemv.hip).
+namespace r4d {
+// The rule of the _parts entries' column starts: 1..4 parts, n0[0] = 0, rising in multiples of 128 below N.
+inline std::string parts_rule(int parts, const int* n0, int N) {
+  if (parts < 1 || parts > 4 || !n0) return "parts must be 1..4 with their first columns n0";
+  if (n0[0] != 0) return "n0[0] must be 0";
+  for (int p = 1; p < parts; ++p)
+    if (n0[p] <= n0[p - 1] || n0[p] >= N || n0[p] % 128) return "n0 must rise in multiples of 128 below N";
+  return "";
+}
+}  // namespace r4d
+
 struct r4d_gemv_args {
   int64_t a0, a1;
   int n_split;

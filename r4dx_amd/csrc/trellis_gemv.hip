@@ -92,12 +92,6 @@ constexpr int kRedRows = 4;          // rows of the final slice sum per pass
 // XF > 0: A0 is the raw input x [M][K] (XF 1: f16, 2: bf16) and the workgroup stages its own slice of the
 // transformed A = f16(FWHT128(fp32(x) * suh) * xscale) (suh0 / suh1 by column part) straight into LDS --
 // the arithmetic of r4dx_trellis_input_*, so A is bit-identical to the unfused path's.
-// The input parts: columns [n_end[p - 1], n_end[p]) read a[p] (n_end[3] is past every column).
-struct R4AParts {
-  const unsigned short* a[4];
-  int n_end[3];
-};
-
 template <int KB, int MT, int NPW, int SK, bool ALDS, int XF, bool WQ = false>
 __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     const R4AParts ap,
@@ -126,9 +120,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
   const int KT = K >> 4, ktw = KT / SKG, kt0 = ky * ktw;
   const unsigned short* __restrict__ A0 = ap.a[0];
   const int n_split = ap.n_end[0];
-  const unsigned short* __restrict__ A = group * 128 < ap.n_end[0] ? ap.a[0]
-                                       : group * 128 < ap.n_end[1] ? ap.a[1]
-                                       : group * 128 < ap.n_end[2] ? ap.a[2] : ap.a[3];
+  const unsigned short* __restrict__ A = r4_part_a(ap, group * 128);
   const int q = lane >> 4, t = (lane >> 3) & 1, c = lane & 7, mrow = lane & 15;
 
   // Steps (4 k-tiles each) of the slice, split into SK contiguous parts of at most nsw steps.
@@ -560,14 +552,8 @@ void launch_gemv(const r4d_gemv_args& a) {
                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     attr = true;
   }
-  R4AParts ap;
-  ap.a[0] = (const unsigned short*)a.a0;
-  ap.a[1] = (const unsigned short*)(a.a1 ? a.a1 : a.a0);
-  ap.a[2] = a.a2 ? (const unsigned short*)a.a2 : ap.a[1];
-  ap.a[3] = a.a3 ? (const unsigned short*)a.a3 : ap.a[2];
-  ap.n_end[0] = a.n_split;
-  ap.n_end[1] = a.a2 ? a.n_end1 : 0x7FFFFFFF;
-  ap.n_end[2] = a.a3 ? a.n_end2 : 0x7FFFFFFF;
+  const R4AParts ap = r4_parts((const void*)a.a0, (const void*)a.a1, a.n_split, (const void*)a.a2, a.n_end1,
+                               (const void*)a.a3, a.n_end2);
   hipLaunchKernelGGL((tq_gemv_kernel<KB, MT, NPW, SK, ALDS, XF, WQ>), grid, block, smem, (hipStream_t)a.stream, ap,
                      (const unsigned*)a.w, (const float*)a.svh, (void*)a.c, (float*)a.ws,
                      (unsigned*)a.tickets, a.M, a.K, a.N, a.SKG, a.full, a.out_scale, (const float*)a.suh0,
@@ -720,13 +706,7 @@ void r4d_trellis_wscale_f32(int64_t w, int64_t scale, int K, int N, int KB, int 
 // the one-part launch of that range at the same SKG.
 const char* r4dx_gemm_trellis_nt_m64_parts_check(int parts, const int* n0, int M, int K, int N, int KB, int SKG,
                                                  int have_ws) {
-  std::string e;
-  if (parts < 1 || parts > 4 || !n0) e = "parts must be 1..4 with their first columns n0";
-  else if (n0[0] != 0) e = "n0[0] must be 0";
-  else {
-    for (int p = 1; p < parts && e.empty(); ++p)
-      if (n0[p] <= n0[p - 1] || n0[p] >= N || n0[p] % 128) e = "n0 must rise in multiples of 128 below N";
-  }
+  const std::string e = r4d::parts_rule(parts, n0, N);
   if (!e.empty()) return r4d::check_result(e);
   return r4d_gemm_trellis_nt_m64_check(M, K, N, parts > 1 ? n0[1] : N, KB, SKG, 1, 1, have_ws);
 }

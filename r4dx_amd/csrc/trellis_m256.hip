@@ -52,8 +52,7 @@ __device__ __forceinline__ int m2_bslot(int n, int c) { return c * 2048 + ((n ^ 
 
 template <int KB, int RT, bool WQ = false>
 __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
-    const unsigned short* __restrict__ A0, const unsigned short* __restrict__ A1, int n_split,
-    const unsigned* __restrict__ W, const float* __restrict__ svh, void* __restrict__ Cv,
+    const R4AParts ap, const unsigned* __restrict__ W, const float* __restrict__ svh, void* __restrict__ Cv,
     float* __restrict__ ws, int M, int K, int N, int SKG, int full, float out_scale,
     const float* __restrict__ wsc, int wq_gsh) {
   constexpr int BLK = 16 * KB;                    // words per (pair, k-tile) block
@@ -67,7 +66,7 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
   const int KT = K >> 4, ktw = KT / SKG, kt0 = ky * ktw;
   const int nst = ktw >> 2;
   const int n0 = group * 128;
-  const unsigned short* __restrict__ A = n0 >= n_split ? A1 : A0;
+  const unsigned short* __restrict__ A = r4_part_a(ap, n0);
 
   if (wave >= 4) {
     // ---- producer p
@@ -374,7 +373,7 @@ std::string m256_check(int M, int K, int N, int n_split, int KB, int SKG) {
 }
 
 template <int KB, int RT, bool WQ>
-void m256_launch_rt(const unsigned short* a0, const unsigned short* a1, int n_split, const unsigned* w,
+void m256_launch_rt(const R4AParts& ap, const unsigned* w,
                     const float* svh, void* c, float* ws, int M, int K, int N, int SKG, int full, float out_scale,
                     const float* wsc, int wq_gsh, hipStream_t st) {
   constexpr unsigned lds = 2 * (32 * RT * 128 + 128 * 128);
@@ -384,44 +383,51 @@ void m256_launch_rt(const unsigned short* a0, const unsigned short* a1, int n_sp
                               (int)lds);
     attr = true;
   }
-  hipLaunchKernelGGL((tq_m256_kernel<KB, RT, WQ>), dim3(N / 128, SKG), dim3(64 * kM2Waves), lds, st, a0, a1, n_split,
+  hipLaunchKernelGGL((tq_m256_kernel<KB, RT, WQ>), dim3(N / 128, SKG), dim3(64 * kM2Waves), lds, st, ap,
                      w, svh, c, ws, M, K, N, SKG, full, out_scale, wsc, wq_gsh);
 }
 template <int KB>
-void m256_launch(int M, const unsigned short* a0, const unsigned short* a1, int n_split, const unsigned* w,
+void m256_launch(int M, const R4AParts& ap, const unsigned* w,
                  const float* svh, void* c, float* ws, unsigned* tickets, int K, int N, int SKG, int full,
                  float out_scale, const float* wsc, int wq_gsh, hipStream_t st) {
   (void)tickets;
   if (wsc) {
     if constexpr (KB == 4 || KB == 5) {
-      if (M == 256) m256_launch_rt<KB, 8, true>(a0, a1, n_split, w, svh, c, ws, M, K, N, SKG, full, out_scale, wsc, wq_gsh, st);
-      else m256_launch_rt<KB, 4, true>(a0, a1, n_split, w, svh, c, ws, M, K, N, SKG, full, out_scale, wsc, wq_gsh, st);
+      if (M == 256) m256_launch_rt<KB, 8, true>(ap, w, svh, c, ws, M, K, N, SKG, full, out_scale, wsc, wq_gsh, st);
+      else m256_launch_rt<KB, 4, true>(ap, w, svh, c, ws, M, K, N, SKG, full, out_scale, wsc, wq_gsh, st);
     }
     return;
   }
-  if (M == 256) m256_launch_rt<KB, 8, false>(a0, a1, n_split, w, svh, c, ws, M, K, N, SKG, full, out_scale, nullptr, 0, st);
-  else m256_launch_rt<KB, 4, false>(a0, a1, n_split, w, svh, c, ws, M, K, N, SKG, full, out_scale, nullptr, 0, st);
+  if (M == 256) m256_launch_rt<KB, 8, false>(ap, w, svh, c, ws, M, K, N, SKG, full, out_scale, nullptr, 0, st);
+  else m256_launch_rt<KB, 4, false>(ap, w, svh, c, ws, M, K, N, SKG, full, out_scale, nullptr, 0, st);
 }
 
-void m256_run(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c, int64_t ws,
-              int64_t tickets, int M, int K, int N, int KB, int SKG, int full, float out_scale, int64_t stream,
-              const char* entry, int64_t wscale = 0, int wq_gsh = 0) {
-  r4d::require(entry, m256_check(M, K, N, n_split, KB, SKG));
-  if (!a0 || !w || !c) r4d::fail(entry, "null A, W or C");
+void m256_run_parts(const R4AParts& ap, int64_t w, int64_t svh, int64_t c, int64_t ws, int64_t tickets, int M,
+                    int K, int N, int KB, int SKG, int full, float out_scale, int64_t stream, const char* entry,
+                    int64_t wscale = 0, int wq_gsh = 0) {
+  r4d::require(entry, m256_check(M, K, N, ap.n_end[0] > N ? N : ap.n_end[0], KB, SKG));
+  if (!ap.a[0] || !w || !c) r4d::fail(entry, "null A, W or C");
   if (full && !svh) r4d::fail(entry, "svh must be non-null");
   if (SKG > 1 && !ws) r4d::fail(entry, "SKG > 1 needs ws");
-  auto A0 = (const unsigned short*)a0, A1 = (const unsigned short*)(a1 ? a1 : a0);
   auto Wp = (const unsigned*)w;
   auto S = (const float*)svh;
   auto WS = (float*)ws;
   auto T = (unsigned*)tickets;
   hipStream_t st = (hipStream_t)stream;
   auto WSC = (const float*)wscale;
-  if (KB == 4) m256_launch<4>(M, A0, A1, n_split, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st);
-  else if (KB == 5) m256_launch<5>(M, A0, A1, n_split, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st);
-  else m256_launch<3>(M, A0, A1, n_split, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st);
+  if (KB == 4) m256_launch<4>(M, ap, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st);
+  else if (KB == 5) m256_launch<5>(M, ap, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st);
+  else m256_launch<3>(M, ap, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st);
   if (SKG > 1) r4d::launch_split_finish(WS, S, (void*)c, M, N, SKG, full, out_scale, st);
   r4d::launch_ok(entry);
+}
+
+void m256_run(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c, int64_t ws,
+              int64_t tickets, int M, int K, int N, int KB, int SKG, int full, float out_scale, int64_t stream,
+              const char* entry, int64_t wscale = 0, int wq_gsh = 0) {
+  r4d::require(entry, m256_check(M, K, N, n_split, KB, SKG));
+  m256_run_parts(r4_parts((const void*)a0, (const void*)a1, n_split), w, svh, c, ws, tickets, M, K, N, KB, SKG, full,
+                 out_scale, stream, entry, wscale, wq_gsh);
 }
 
 }  // namespace
@@ -459,6 +465,28 @@ size_t r4d_gemm_trellis_nt_m256_ws_bytes(int M, int N, int SKG) {
   return (size_t)SKG * (size_t)M * (size_t)N * sizeof(float);
 }
 
+// No reference counterpart: r4d_gemm_trellis_nt_m256 over up to four input parts (the prefill form of
+// r4dx_gemm_trellis_nt_m64_parts): columns [n0[p], n0[p + 1]) read a[p]. Every column equals the one-part launch
+// of its range at the same SKG.
+const char* r4dx_gemm_trellis_nt_m256_parts_check(int parts, const int* n0, int M, int K, int N, int KB, int SKG) {
+  std::string e = r4d::parts_rule(parts, n0, N);
+  if (e.empty()) e = m256_check(M, K, N, parts > 1 ? n0[1] : N, KB, SKG);
+  return r4d::check_result(e);
+}
+void r4dx_gemm_trellis_nt_m256_parts(const int64_t* a, const int* n0, int parts, int64_t w, int64_t svh, int64_t c,
+                                     int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SKG,
+                                     float out_scale, int64_t stream) {
+  const char* e = "gemm_trellis_nt_m256_parts";
+  if (!a || !n0) r4d::fail(e, "null part arrays");
+  if (const char* m = r4dx_gemm_trellis_nt_m256_parts_check(parts, n0, M, K, N, KB, SKG)) r4d::fail(e, m);
+  for (int p = 0; p < parts; ++p)
+    if (!a[p]) r4d::fail(e, "null part input");
+  const R4AParts ap = r4_parts((const void*)a[0], parts > 1 ? (const void*)a[1] : nullptr, parts > 1 ? n0[1] : N,
+                               parts > 2 ? (const void*)a[2] : nullptr, parts > 2 ? n0[2] : 0,
+                               parts > 3 ? (const void*)a[3] : nullptr, parts > 3 ? n0[3] : 0);
+  m256_run_parts(ap, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale, stream, e);
+}
+
 void r4d_gemm_trellis_nt_m256_raw(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t c, int64_t ws,
                                   int64_t tickets, int M, int K, int N, int KB, int SKG, int64_t stream) {
   m256_run(a0, a1, n_split, w, 0, c, ws, tickets, M, K, N, KB, SKG, 0, 1.f, stream, "gemm_trellis_nt_m256_raw");
@@ -481,7 +509,7 @@ void r4d_gemm_trellis_nt_m256_wq(int64_t a0, int64_t a1, int n_split, int64_t w,
 }
 
 // This build's K split for the prefill GEMM: the workgroup count per CU decides the critical path
-// (at most two resident per CU, sharing its MFMA pipes), so SKG minimises ceil(G SKG / CUs) x steps
+// (one resident per CU: the two LDS stages take 96 KiB), so SKG minimises ceil(G SKG / CUs) x steps
 // per slice plus the cost of the second pass (SKG x M x N fp32 written and read back).
 int r4d_mi355x_trellis_m256_skg(int K, int N, int KB) {
   (void)KB;
@@ -498,8 +526,9 @@ int r4d_mi355x_trellis_m256_skg(int K, int N, int KB) {
     if (KT % (4 * d)) continue;
     const double rounds = (double)(((long long)G * d + cus - 1) / cus);
     const double steps = (double)KT / (4 * d);
-    // one step ~ 0.43 us of MFMA; partials ~ 256 * 128 * 4 * 2 bytes per workgroup-slice at ~6 TB/s
-    const double cost = rounds * steps * 0.43 + (d > 1 ? (double)G * d * 262144.0 / 6e6 + 2.0 : 0.0);
+    // measured on config 2's shapes (M = 256, one workgroup per CU): a step ~1.05 us per round; a split costs
+    // ~2 us (the finish launch) plus ~0.06 us per workgroup-slice (its partials written and read back)
+    const double cost = rounds * steps * 1.05 + (d > 1 ? 2.0 + 0.06 * G * d : 0.0);
     if (cost < best_cost) {
       best_cost = cost;
       best = d;

@@ -68,6 +68,8 @@ SIGS = {
     "r4dx_fwht128_f32": (None, [I64, I64, I32, I64]),
     "r4dx_gemm_trellis_nt_m64_parts_check": (CSTR, [I32, I32P, I32, I32, I32, I32, I32, I32]),
     "r4dx_gemm_trellis_nt_m64_parts": (None, [I64P, I32P, I32] + [I64] * 5 + [I32] * 5 + [F32, I64]),
+    "r4dx_gemm_trellis_nt_m256_parts_check": (CSTR, [I32, I32P, I32, I32, I32, I32, I32]),
+    "r4dx_gemm_trellis_nt_m256_parts": (None, [I64P, I32P, I32] + [I64] * 5 + [I32] * 5 + [F32, I64]),
     "r4d_trellis_wscale_count": (SZ, [I32, I32, I32]),
     "r4d_trellis_wscale_f32": (None, [I64, I64, I32, I32, I32, I32, I64]),
     "r4d_gemm_trellis_nt_m64_wq": (None, [I64, I64, I32, I64, I64, I64, I64, I64] + [I32] * 11 + [F32, I64, I32, I64]),

@@ -121,3 +121,32 @@ def test_config2_shapes(name, K, N):
         q = O.decode_pair_grid(words, K, N, KB)
         ref = _ref_f64(a, q)
         assert close_rel(raw.cpu().numpy(), ref, 1e-3, 1e-4) <= 1.0, KB
+
+
+@pytest.mark.parametrize("M,KB,widths", [(256, 4, (6144, 1024, 1024)), (128, 5, (256, 128, 384, 256)),
+                                         (256, 5, (10240, 6144))])
+def test_m256_parts_equals_one_launch_per_projection(M, KB, widths):
+    """r4dx_gemm_trellis_nt_m256_parts: every column equals its projection's own M = 256 launch at the same SKG,
+    byte for byte; and the whole against the fp64 oracle's linear (bf16 bar)."""
+    banner("m256 parts", M, KB, widths)
+    K = 5120 if widths[0] > 1024 else 1024
+    N = sum(widths)
+    n0 = [int(x) for x in np.concatenate([[0], np.cumsum(widths)[:-1]])]
+    words, _, svh = WL.trellis_linear(K, N, KB, 5 * M + KB)
+    a = [WL.activations_f16(M, K, 80 + p, outlier_frac=0.01).view(np.uint16) for p in range(len(widths))]
+    a_d = [dev(x) for x in a]
+    skg = api.trellis_m256_skg(K, N, KB)
+    osc = float(np.float32(1.0 / np.sqrt(128.0)))
+    whole = host_u16(api.trellis_gemm_m256_parts(a_d, n0, dev(words), dev(svh), K, N, KB, skg=skg, out_scale=osc))
+    grid = words.reshape(N // 32, -1)
+    check_oracle = N * K <= 8192 * 5120
+    q = O.decode_pair_grid(words, K, N, KB) if check_oracle else None
+    for p, (c0, wdt) in enumerate(zip(n0, widths)):
+        w_p = np.ascontiguousarray(grid[c0 // 32:(c0 + wdt) // 32]).ravel()
+        one = host_u16(api.trellis_gemm_m256(a_d[p], dev(w_p), dev(svh[c0:c0 + wdt]), K, wdt, KB, skg=skg,
+                                             out_scale=osc))
+        torch.cuda.synchronize()
+        assert np.array_equal(whole[:, c0:c0 + wdt], one), p
+        if check_oracle and p > 0:
+            ref = O.linear_from_a(a[p], np.ascontiguousarray(q[:, c0:c0 + wdt]), svh[c0:c0 + wdt])
+            assert close_rel(O.bf16_bits_to_f32(whole[:, c0:c0 + wdt]), ref, 2.0**-8, 1e-3) <= 1.0
