@@ -87,7 +87,7 @@ __device__ __forceinline__ void load_words_ptr(Words<KB>& s, const unsigned* __r
 // Weights are prefetched PF steps ahead (a step is 4 k-tiles = one dwordx4 per lane) and issued before
 // A is staged in LDS.
 constexpr int kRedParts = 8;         // the final slice sum is 8 interleaved runs, added in order
-constexpr int kRedRows = 4;          // rows of the final slice sum per pass
+constexpr int kRedRows = 4;          // rows of the final slice sum per pass (8 measured slower at M = 8: LDS)
 
 // XF > 0: A0 is the raw input x [M][K] (XF 1: f16, 2: bf16) and the workgroup stages its own slice of the
 // transformed A = f16(FWHT128(fp32(x) * suh) * xscale) (suh0 / suh1 by column part) straight into LDS --
@@ -286,14 +286,29 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
   } else if constexpr (ALDS) {
     // chunk (ktl, row, j): k 16 (kt0 + ktl) + 8j .. + 8 of A[row] -> halves of fragments h = 0, 1;
     // k-tiles past the slice are zero, and so is the 32-byte block after the copy (rows >= M read it).
+    // kStageU chunks per thread per pass, all loads issued before any is written: one memory round trip
+    // per pass, not one per chunk (at M = 8 and up a workgroup stages several chunks per thread)
+    constexpr int kStageU = 4;
     const int chunks = ktl_pad * M * 2;
-    for (int i = threadIdx.x; i < chunks + 2; i += NT) {
-      r4u4 v = {0u, 0u, 0u, 0u};
-      const int j = i & 1, rm = i >> 1, r = rm % M, ktl = rm / M;
-      if (i < chunks && ktl < ktw) v = *(const r4u4*)(A + (size_t)r * K + 16 * (kt0 + ktl) + 8 * j);
-      r4u2* dst = (r4u2*)(alds + (size_t)rm * 2);
-      dst[j] = (r4u2){v[0], v[1]};        // h = 0, elements 4j .. 4j + 3
-      dst[2 + j] = (r4u2){v[2], v[3]};    // h = 1
+    for (int i0 = threadIdx.x; i0 < chunks + 2; i0 += kStageU * NT) {
+      r4u4 v[kStageU];
+#pragma unroll
+      for (int u = 0; u < kStageU; ++u) {
+        const int i = i0 + u * NT;
+        const int j = i & 1, rm = i >> 1, r = rm % M, ktl = rm / M;
+        v[u] = (r4u4){0u, 0u, 0u, 0u};
+        if (i < chunks && ktl < ktw) v[u] = *(const r4u4*)(A + (size_t)r * K + 16 * (kt0 + ktl) + 8 * j);
+      }
+#pragma unroll
+      for (int u = 0; u < kStageU; ++u) {
+        const int i = i0 + u * NT;
+        if (i < chunks + 2) {
+          const int j = i & 1, rm = i >> 1;
+          r4u2* dst = (r4u2*)(alds + (size_t)rm * 2);
+          dst[j] = (r4u2){v[u][0], v[u][1]};        // h = 0, elements 4j .. 4j + 3
+          dst[2 + j] = (r4u2){v[u][2], v[u][3]};    // h = 1
+        }
+      }
     }
     __syncthreads();
   }
