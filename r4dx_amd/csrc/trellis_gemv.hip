@@ -290,7 +290,17 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     // per pass, not one per chunk (at M = 8 and up a workgroup stages several chunks per thread)
     constexpr int kStageU = 4;
     const int chunks = ktl_pad * M * 2;
-    for (int i0 = threadIdx.x; i0 < chunks + 2; i0 += kStageU * NT) {
+    if (chunks + 2 <= NT) {   // one chunk per thread at most (M = 1, 2): no unrolled address arithmetic
+      const int i = threadIdx.x;
+      if (i < chunks + 2) {
+        r4u4 v = {0u, 0u, 0u, 0u};
+        const int j = i & 1, rm = i >> 1, r = rm % M, ktl = rm / M;
+        if (i < chunks && ktl < ktw) v = *(const r4u4*)(A + (size_t)r * K + 16 * (kt0 + ktl) + 8 * j);
+        r4u2* dst = (r4u2*)(alds + (size_t)rm * 2);
+        dst[j] = (r4u2){v[0], v[1]};
+        dst[2 + j] = (r4u2){v[2], v[3]};
+      }
+    } else for (int i0 = threadIdx.x; i0 < chunks + 2; i0 += kStageU * NT) {
       r4u4 v[kStageU];
 #pragma unroll
       for (int u = 0; u < kStageU; ++u) {
