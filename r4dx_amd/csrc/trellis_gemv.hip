@@ -816,26 +816,37 @@ void r4d_trellis_reconstruct_f16(int64_t w, int64_t q, int K, int N, int KB, int
   r4d::launch_ok(entry);
 }
 
-// This build's split choice for the GEMV, measured on MI355X over the 27B shapes (KB 4 and 5, M = 1 and
-// 8): the launch time is flat within a few per cent for 16..40 k-tiles per wave, so SKG is the divisor of
-// K/16 (2..32) that gives each of a slice's 4 waves closest to 28 k-tiles (log distance; ties to the
-// larger SKG). Independent of M, so every M <= 16 gets the same row bits.
+// This build's split choice for the GEMV, measured on MI355X over the 27B shapes and their same-input merges
+// (KB 4, M = 1 and 8): among the divisors of K/16 (2..32) that leave each of a slice's 4 waves at least 16
+// k-tiles, the ones that launch at least 6 waves per CU are preferred, and of those the one closest to 32
+// k-tiles per wave (log distance; ties to the larger SKG); with none, the largest. E.g. K = 5120: SKG 2 from
+// N = 6144 on (16384 columns: 18.2 us against 20.1 at SKG 4), 5 for N = 1024; K = 6144, N = 5120: 3.
+// Depends on the shape only, so every M <= 16 gets the same row bits.
 int r4d_mi355x_trellis_gemv_skg(int K, int N, int KB) {
   (void)KB;
   const int KT = K / 16;
   if (KT <= 0 || N <= 0) return 1;
-  int best = 1;
+  int cus = 256, dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
+  }
+  const long long want = 6LL * cus;
+  int best = 0, fallback = 1;
   double best_d = 1e30;
   for (int d = 2; d <= 32 && d <= KT; ++d) {
     if (KT % d) continue;
     const double per_wave = (double)KT / d / 4.0;
-    const double dist = per_wave > 28.0 ? per_wave / 28.0 : 28.0 / per_wave;
+    if (per_wave < 16.0) continue;
+    fallback = d;
+    if ((long long)(N / 32) * 4 * d < want) continue;
+    const double dist = per_wave > 32.0 ? per_wave / 32.0 : 32.0 / per_wave;
     if (dist <= best_d) {
       best = d;
       best_d = dist;
     }
   }
-  return best;
+  return best ? best : fallback;
 }
 
 }  // extern "C"
