@@ -654,9 +654,34 @@ def cpu_baseline(KB):
         if time.perf_counter() - t0 > 10.0 or reps >= 20:
             break
     dt = (time.perf_counter() - t0) / reps
-    return {"value": round(K * N * KB / 8 / dt / 1e9, 4), "unit": "GB/s", "cores": cores,
+    port = {"value": round(K * N * KB / 8 / dt / 1e9, 4), "unit": "GB/s", "cores": cores,
             "kind": "port", "sample": f"config0 K=N=5120 KB={KB} M=1: transform + decode + fp64 linear, "
                                       f"{reps} runs, {dt * 1e3:.1f} ms each"}
+    ref = O.ref()
+    if ref is None:
+        return port
+    # the reference's own CPU path (tests/kernels/trellis_ref.hpp compiled into oracle/_ref), single-threaded as
+    # it is written: input transform, pair-grid decode, fp64 linear
+    from oracle_lib import ptr
+    xb = O.f32_to_bf16_bits(O.f16_bits_to_f32(x))
+    a = np.empty((1, K), np.uint16)
+    q = np.empty((K, N), np.uint16)
+    y = np.empty((1, N), np.float64)
+    svh32 = np.ascontiguousarray(svh, np.float32)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        ref.ref_transform_input_bf16(ptr(xb), 1, K, ptr(np.ascontiguousarray(suh, np.float32)), 0, ptr(a))
+        ref.ref_decode_pair_grid(ptr(words), K, N, KB, ptr(q))
+        ref.ref_linear_from_a(ptr(a), None, N, 1, K, N, ptr(q), ptr(svh32), 0, ptr(y))
+        reps += 1
+        if time.perf_counter() - t0 > 15.0 or reps >= 10:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    return {"value": round(K * N * KB / 8 / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "reference",
+            "sample": f"config0 K=N=5120 KB={KB} M=1 (bf16 x): the reference's trellis_ref.hpp transform + "
+                      f"pair-grid decode + fp64 linear, single-threaded as written, {reps} runs, {dt * 1e3:.1f} ms "
+                      f"each", "port_all_cores": port}
 
 
 if __name__ == "__main__":
