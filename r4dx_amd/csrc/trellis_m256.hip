@@ -286,74 +286,85 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
   }
 }
 
-// The split form's second pass: a workgroup per (128-column group, 32 rows) sums the SKG slices of
-// ws in slice order (coalesced: a thread per column, 16 rows each) into LDS, then one wave per row
-// applies the group's FWHT-128 (r4_fwht128_wave, the reference's stage order), svh, out_scale and
-// the bf16 rounding -- or, raw, stores the fp32 sums.
+// The split form's second pass: a workgroup per (128-column group, 16 rows) sums the SKG slices of ws in
+// slice order into LDS, then one wave per row applies the group's FWHT-128 (r4_fwht128_wave, the reference's
+// stage order), svh, out_scale and the bf16 rounding -- or, raw, stores the fp32 sums. Up to 8 slices (one per
+// run): a thread takes 4 adjacent columns of 2 rows and requests all 8 slices of them at once as 16-byte
+// loads (a slice past SKG reads past the buffer and returns 0, which is exactly what an empty run adds), so
+// one memory round trip covers the workgroup; more slices take the general loop (a thread per column).
+constexpr int kFinRows = 16;
 __global__ __launch_bounds__(256) void tq_m256_finish(const float* __restrict__ ws, const float* __restrict__ svh,
                                                       void* __restrict__ Cv, int M, int N, int SKG, int full,
                                                       float out_scale) {
-  __shared__ float sums[32][128];
-  const int group = blockIdx.x, r0 = blockIdx.y * 32;
-  const int col = threadIdx.x & 127, rh = threadIdx.x >> 7;
+  __shared__ float sums[kFinRows][128];
+  const int group = blockIdx.x, r0 = blockIdx.y * kFinRows;
   const int n0 = group * 128;
   const size_t sy = (size_t)M * N;
   // the M <= 64 kernel's slice order: run p (0..7) = 0.f + slices p, p + 8, ... in order, then the 8 runs
-  // added in order 0..7. Up to 8 slices (one per run), each thread requests all slices of 8 of its rows
-  // at once (buffer loads: a slice past SKG reads past the buffer and returns 0, which is exactly what an
-  // empty run adds); more slices take the general loop.
-  float v[16];
+  // added in order 0..7
   if (SKG <= 8) {
+    const int cq = threadIdx.x & 31, rr = threadIdx.x >> 5;      // columns 4 cq .. 4 cq + 3, rows rr, rr + 8
     const unsigned sy4 = (unsigned)sy * 4u;
     const r4_rsrc wr = mk_rsrc(ws, (unsigned)SKG * sy4);
+    r4f4 t[8][2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float t[8][8];
+    for (int p = 0; p < 8; ++p)
 #pragma unroll
-      for (int p = 0; p < 8; ++p)
+      for (int u = 0; u < 2; ++u) {
+        const unsigned off = (unsigned)p * sy4 + (unsigned)((r0 + rr + 8 * u) * N + n0 + 4 * cq) * 4u;
+        t[p][u] = __builtin_bit_cast(r4f4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+      }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const unsigned off = (unsigned)p * sy4 + (unsigned)((r0 + rh + 2 * (8 * h + u)) * N + n0 + col) * 4u;
-          t[p][u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0));
-        }
+    for (int u = 0; u < 2; ++u) {
+      float v[4];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        float acc = 0.f + t[0][u];
+      for (int e = 0; e < 4; ++e) {
+        float acc = 0.f + t[0][u][e];
 #pragma unroll
-        for (int p = 1; p < 8; ++p) acc = acc + (0.f + t[p][u]);
-        v[8 * h + u] = acc;
+        for (int p = 1; p < 8; ++p) acc = acc + (0.f + t[p][u][e]);
+        v[e] = acc;
+      }
+      const int r = rr + 8 * u;
+      if (!full) {
+        *(r4f4*)((float*)Cv + (size_t)(r0 + r) * N + n0 + 4 * cq) = (r4f4){v[0], v[1], v[2], v[3]};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sums[r][4 * cq + e] = v[e];
       }
     }
+    if (!full) return;
   } else {
+    const int col = threadIdx.x & 127, rh = threadIdx.x >> 7;   // rows rh + 2 u
+    float v[kFinRows / 2];
 #pragma unroll 1
     for (int p = 0; p < 8; ++p) {
-      float run[16];
+      float run[kFinRows / 2];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) run[u] = 0.f;
+      for (int u = 0; u < kFinRows / 2; ++u) run[u] = 0.f;
       for (int y = p; y < SKG; y += 8) {
-        float t[16];
+        float t[kFinRows / 2];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) t[u] = ws[(size_t)y * sy + (size_t)(r0 + rh + 2 * u) * N + n0 + col];
+        for (int u = 0; u < kFinRows / 2; ++u) t[u] = ws[(size_t)y * sy + (size_t)(r0 + rh + 2 * u) * N + n0 + col];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) run[u] += t[u];
+        for (int u = 0; u < kFinRows / 2; ++u) run[u] += t[u];
       }
 #pragma unroll
-      for (int u = 0; u < 16; ++u) v[u] = p == 0 ? run[u] : v[u] + run[u];
+      for (int u = 0; u < kFinRows / 2; ++u) v[u] = p == 0 ? run[u] : v[u] + run[u];
     }
-  }
-  if (!full) {
-    float* Cf = (float*)Cv;
+    if (!full) {
+      float* Cf = (float*)Cv;
 #pragma unroll
-    for (int u = 0; u < 16; ++u) Cf[(size_t)(r0 + rh + 2 * u) * N + n0 + col] = v[u];
-    return;
-  }
+      for (int u = 0; u < kFinRows / 2; ++u) Cf[(size_t)(r0 + rh + 2 * u) * N + n0 + col] = v[u];
+      return;
+    }
 #pragma unroll
-  for (int u = 0; u < 16; ++u) sums[rh + 2 * u][col] = v[u];
+    for (int u = 0; u < kFinRows / 2; ++u) sums[rh + 2 * u][col] = v[u];
+  }
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   unsigned short* Cb = (unsigned short*)Cv;
   const float sv0 = svh[n0 + lane], sv1 = svh[n0 + lane + 64];
-  for (int r = wave; r < 32; r += 4) {
+  for (int r = wave; r < kFinRows; r += 4) {
     float v0 = sums[r][lane], v1 = sums[r][lane + 64];
     r4_fwht128_wave(v0, v1, lane);
     const float y0 = v0 * sv0, y1 = v1 * sv1;
@@ -434,7 +445,7 @@ void m256_run(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64
 
 void r4d::launch_split_finish(const float* ws, const float* svh, void* c, int M, int N, int SKG, int full,
                               float out_scale, hipStream_t st) {
-  hipLaunchKernelGGL(tq_m256_finish, dim3(N / 128, M / 32), dim3(256), 0, st, ws, svh, c, M, N, SKG, full, out_scale);
+  hipLaunchKernelGGL(tq_m256_finish, dim3(N / 128, M / kFinRows), dim3(256), 0, st, ws, svh, c, M, N, SKG, full, out_scale);
 }
 
 static const char* const sk_msg =
