@@ -59,3 +59,20 @@ def test_plans_of_the_tp2_rank_shapes(N, K, parts, n0, kb):
     assert m256.ok and (K // 16) % m256.SKG == 0
     i8 = plan.plan_trellis_i8(N, K, kb, parts=parts, part_n0=n0)
     assert i8.ok
+
+
+@pytest.mark.parametrize("K,N", [(5120, 16384), (5120, 8192), (5120, 34816), (6144, 5120), (17408, 5120),
+                                 (5120, 1024), (1024, 512), (8704, 5120), (3072, 5120)])
+def test_gemv_split_planner_rules(K, N):
+    """r4d_mi355x_trellis_gemv_skg: a divisor of K/16 (whole k-tiles per slice), at least 16 k-tiles per wave of a
+    slice when any split allows it, and the documented picks on the step's launch shapes."""
+    from r4dx_amd import api
+    skg = api.trellis_gemv_skg(K, N, 4)
+    KT = K // 16
+    assert KT % skg == 0
+    if skg > 1:
+        assert KT / skg / 4 >= 16
+    want = {(5120, 16384): 2, (5120, 8192): 2, (5120, 34816): 2, (6144, 5120): 3, (17408, 5120): 8,
+            (5120, 1024): 5, (1024, 512): 1}
+    if (K, N) in want:
+        assert skg == want[(K, N)]
