@@ -137,7 +137,8 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
   float* part_acc = (float*)(lds_raw + a_vec);                       // [(SK-1) * NPW][8 MT][64]
   float* red = part_acc + (size_t)(SK - 1) * NPW * 8 * MT * 64;      // [M][128]
   float* runs = red + (size_t)M * 128;                               // [8][4][128]
-  int* flag = (int*)(runs + (size_t)kRedParts * kRedRows * 128);
+  const int red_rows = min(kRedRows, M);      // rows per finish pass (the LDS holds no more)
+  int* flag = (int*)(runs + (size_t)kRedParts * red_rows * 128);
 
   const unsigned* __restrict__ wpair = W + ((size_t)pair * KT + kt0) * BLK;
   const r4_rsrc wr = r4_make_rsrc(wpair, (unsigned)ktw * BLK * 4u);
@@ -428,8 +429,8 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     const unsigned sy4 = (unsigned)M * (unsigned)N * 4u;
     const r4_rsrc wsr = r4_make_rsrc(ws, (unsigned)SKG * sy4);
     constexpr int kFinItems = 4;
-    for (int r0 = 0; r0 < M; r0 += kRedRows) {
-      const int rows = min(kRedRows, M - r0);
+    for (int r0 = 0; r0 < M; r0 += red_rows) {
+      const int rows = min(red_rows, M - r0);
       const int items = kRedParts * rows * 128;
       for (int b0 = 0; b0 < items; b0 += kFinItems * NT) {
         float tv[kFinItems][8];
@@ -454,7 +455,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
             float v = 0.f;
 #pragma unroll
             for (int u = 0; u < 8; ++u) v += tv[it][u];
-            runs[(size_t)p * kRedRows * 128 + e] = v;
+            runs[(size_t)p * red_rows * 128 + e] = v;
           }
         }
       }
@@ -462,7 +463,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
       for (int e = threadIdx.x; e < rows * 128; e += NT) {
         float v = runs[e];
 #pragma unroll
-        for (int p = 1; p < kRedParts; ++p) v += runs[(size_t)p * kRedRows * 128 + e];
+        for (int p = 1; p < kRedParts; ++p) v += runs[(size_t)p * red_rows * 128 + e];
         if (full) red[(size_t)r0 * 128 + e] = v;
         else Cf[(size_t)(r0 + (e >> 7)) * N + n0 + (e & 127)] = v;
       }
@@ -559,7 +560,7 @@ __global__ __launch_bounds__(256) void tq_wscale_kernel(const unsigned* __restri
 size_t gemv_ktl_pad(int SK, int ktw) { return (size_t)SK * ((((ktw + 3) >> 2) + SK - 1) / SK) * 4; }
 size_t gemv_lds(int MT, int NPW, int SK, bool alds, int ktw, int M) {
   return (alds ? gemv_ktl_pad(SK, ktw) * M * 32 + 32 : 0) + (size_t)(SK - 1) * NPW * 8 * MT * 64 * 4 +
-         (size_t)(M + kRedParts * kRedRows) * 128 * 4 + 16;
+         (size_t)(M + kRedParts * (M < kRedRows ? M : kRedRows)) * 128 * 4 + 16;
 }
 constexpr size_t kAldsMax = 48 * 1024;   // A slices up to this many bytes are staged in LDS
 
