@@ -62,13 +62,14 @@ def trellis_gemm_m64(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out=
                                           int(svh is not None), int(ws is not None and tickets is not None))
     if msg:
         raise ValueError(msg.decode())
-    if out is None:
-        out = torch.empty((M, N), dtype=torch.float32 if raw else torch.bfloat16, device=a0.device)
-    st = _stream(stream)
     if wq is not None:
         if clk is not None:
             raise ValueError("the _wq entries take no clock probe")
         tab, gsh = _wq_args(wq, K, KB)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32 if raw else torch.bfloat16, device=a0.device)
+    st = _stream(stream)
+    if wq is not None:
         if raw:
             L.r4d_gemm_trellis_nt_m64_raw_wq(_p(a0), _p(a1), n_split, _p(w), _p(out), _p(ws), _p(tickets),
                                              M, K, N, KB, 0, sk, 0, 0, skg, 0, 0, tab, gsh, st)
@@ -148,6 +149,10 @@ def trellis_gemm_m256(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out
     msg = L.r4d_gemm_trellis_nt_m256_check(M, K, N, n_split, KB, 0, 0, skg, 0, 0)
     if msg:
         raise ValueError(msg.decode())
+    if wq is not None:
+        if raw:
+            raise ValueError("r4d_gemm_trellis_nt_m256_wq has no raw form")
+        _wq_args(wq, K, KB)
     if ws is None and skg > 1:
         ws = torch.empty(L.r4d_gemm_trellis_nt_m256_ws_bytes(M, N, skg) // 4, dtype=torch.float32,
                          device=a0.device)

@@ -101,3 +101,20 @@ def test_parts_check(L):
     assert b"parts" in L.r4dx_gemm_trellis_nt_m64_parts_check(5, (C.c_int * 5)(0, 128, 256, 384, 512), 1, 1024,
                                                               1024, 4, 1, 1)
     assert b"M must be" in chk([0, 256], M=65)
+
+
+def test_parts_wrappers_refuse_before_launch():
+    """api.trellis_gemm_m64_parts / _m256_parts apply the entries' rules first: a bad column start raises
+    ValueError in Python (CPU tensors: nothing reaches a device)."""
+    torch = pytest.importorskip("torch")
+    from r4dx_amd import api
+    a = [torch.zeros((1, 1024), dtype=torch.float16) for _ in range(2)]
+    w = torch.zeros(1024 * 512 * 4 // 32, dtype=torch.int32)
+    svh = torch.ones(512)
+    with pytest.raises(ValueError, match="n0"):
+        api.trellis_gemm_m64_parts(a, [0, 100], w, svh, 1024, 512, 4, skg=1)
+    a256 = [torch.zeros((256, 1024), dtype=torch.float16) for _ in range(2)]
+    with pytest.raises(ValueError, match="n0"):
+        api.trellis_gemm_m256_parts(a256, [0, 512], w, svh, 1024, 512, 4, skg=1)
+    with pytest.raises(ValueError, match="gsh"):
+        api.trellis_gemm_m64(a[0], w, svh, 1024, 512, 4, skg=1, wq=(svh, 4))
