@@ -480,12 +480,12 @@ def bench_w4a16(api, WL, R=4):
                         api.argmax_rows(out, idx, val)
             times = {}
             for with_am in (False, True):
-                run(with_am)
-                torch.cuda.synchronize()
                 gr = torch.cuda.CUDAGraph()
                 s = torch.cuda.Stream()
                 s.wait_stream(torch.cuda.current_stream())
                 with torch.cuda.stream(s):
+                    run(with_am)   # eager once on the capture stream: the argmax allocates its scratch there
+                    torch.cuda.synchronize()
                     with torch.cuda.graph(gr, stream=s):
                         for _ in range(R):
                             run(with_am)

@@ -9,10 +9,13 @@
  *
  * Tuning knobs of the reference signatures (WV, MT, NP, U, NT, skw) are accepted and ignored:
  * this build plans its own geometry.  SKG (the grid K split) is honoured, because the caller sizes
- * ws by it.  SK of the M <= 64 GEMM chooses the summation order: SK = 1 runs one wave per tile pair
- * over the whole K slice (the order r4d_gemm_trellis_nt_m256 reproduces); any other SK, with ws and
- * tickets given or SKG > 1, splits each slice over 4 waves added in k order (an unsplit launch without
- * ws always runs the SK = 1 form).  Results depend on (K, N, KB, SKG, that form) and never on M.
+ * ws by it.  SK of the M <= 64 GEMM chooses the summation order: SK = 1 or 2 runs one wave per tile
+ * pair over the whole K slice (the order r4d_gemm_trellis_nt_m256 reproduces, so the engine's
+ * PlanTrellisM256 -- which asks for a K-slice grouping skw <= SK, src/model/linear.cpp:705-722 -- can
+ * plan an M = 64 row of SK 2); any other SK (0, 4, 8, 16), with ws and tickets given or SKG > 1, splits
+ * each slice over 4 waves added in k order (an unsplit launch without ws always runs the one-wave form).
+ * Results depend on (K, N, KB, SKG, that form) and never on M.  The MI355X tuning rows in the engine's
+ * own formats are r4dx_amd/tables/ *.inc.
  */
 #ifndef R4D_MI355X_H
 #define R4D_MI355X_H
@@ -26,7 +29,8 @@ extern "C" {
 /* ---- trellis GEMV / skinny GEMM, M = 1..64 ----------------------------------------------------- */
 /* third_party/libr4d/r4d.h:372-375 r4d_gemm_trellis_nt_m64: C bf16 [M][N] =
  * bf16((FWHT128(A_p(n) @ Q) * svh) * out_scale); A f16 [M][K] (a1 = 0: a0), W the pair-grid words,
- * ws fp32 ws_bytes(M, N, SKG), tickets u32 [N/128] zeroed before first use (self-resetting). */
+ * ws fp32 ws_bytes(M, N, SKG) (SKG M N 4 at most 2 GiB), tickets tickets_bytes(N) (one 128-byte line per
+ * 128-column group) zeroed before first use (self-resetting). */
 void r4d_gemm_trellis_nt_m64(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
                              int64_t ws, int64_t tickets, int M, int K, int N, int KB, int WV, int SK,
                              int MT, int NP, int SKG, int U, int NT, float out_scale, int64_t stream);
@@ -39,7 +43,7 @@ void r4d_gemm_trellis_nt_m64_raw(int64_t a0, int64_t a1, int n_split, int64_t w,
 int    r4d_gemm_trellis_nt_m64_has_rate(int KB);                 /* r4d.h:384 */
 int    r4d_gemm_trellis_nt_m64_max_m(void);                      /* r4d.h:385 */
 size_t r4d_gemm_trellis_nt_m64_ws_bytes(int M, int N, int SKG);  /* r4d.h:386 */
-size_t r4d_gemm_trellis_nt_m64_tickets_bytes(int N);             /* r4d.h:387 */
+size_t r4d_gemm_trellis_nt_m64_tickets_bytes(int N);             /* r4d.h:387: N/128 lines of 128 B */
 void   r4d_gemm_trellis_nt_m64_zero_tickets(int64_t tickets, size_t bytes, int64_t stream); /* r4d.h:389 */
 /* r4d.h:390-393: the whole decoded Q[K][N] f16 bits, bit-exact against the format's decode. */
 void   r4d_trellis_reconstruct_f16(int64_t w, int64_t q, int K, int N, int KB, int64_t stream);
@@ -64,8 +68,9 @@ const char* r4dx_trellis_gemv_xf_check(int M, int K, int N, int n_split, int KB,
  * (two launches when SKG > 1: the slices, then their sum and the epilogue); ws fp32 ws_bytes(M, N,
  * SKG) required when SKG > 1 (the reference always requires it); tickets accepted and unused;
  * (K/16) must be divisible by 4 SKG. Every element equals, bit for bit, r4d_gemm_trellis_nt_m64's at
- * M = 64 with SK = 1 and the same SKG (r4d.h:402-412); SK must be 0 or 1 (0 means 1), since SK > 1 names
- * the 4-wave split order, which this kernel does not reproduce (_check says so). NP, U, skw unused. */
+ * M = 64 with the same SK and SKG (r4d.h:402-412); SK must be 0, 1 or 2 (0 means 1: the one-wave-per-pair
+ * order), since SK 4, 8, 16 name the 4-wave split order, which this kernel does not reproduce (_check says
+ * so). NP, U, skw unused. */
 void r4d_gemm_trellis_nt_m256(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
                               int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SK, int NP,
                               int SKG, int U, float out_scale, int64_t stream, int skw);
@@ -103,8 +108,10 @@ void r4d_gemm_w4a16_nt_m64_f32(int group, int64_t a, int64_t wq, int64_t wsz, in
 
 /* ---- argmax (src/kernels/include/r4dx/kernels/kernels.h:297-330) -------------------------------- */
 /* out_idx[0] = argmax over logits[0, vocab): larger value first, then lower index; a NaN never wins,
- * a row with nothing above -inf gives index 0 (argmax_ref.hpp:22-41). Two launches over a
- * library-owned per-device partial buffer: calls that overlap on one device race. */
+ * a row with nothing above -inf gives index 0 (argmax_ref.hpp:22-41). One launch; its partial keys and
+ * tickets live in a scratch per (device, stream) that the library allocates at the stream's first argmax
+ * (so that first call must not be under graph capture) and keeps, as the reference keeps its partials per
+ * stream (r4dx_kernels.hip:1715-1734): calls on different streams never share it. */
 void r4dx_argmax_f32(int64_t logits, int64_t out_idx, int64_t vocab, int64_t stream);          /* :308 */
 void r4dx_argmax_val_f32(int64_t logits, int64_t out_idx, int64_t out_val, int64_t vocab,
                          int64_t stream);                                                       /* :316 */

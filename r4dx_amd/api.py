@@ -19,11 +19,12 @@ def _stream(stream=None):
 
 
 class TicketBuffer:
-    """The per-linear ticket words of the split GEMMs (zeroed once; every complete launch leaves
-    them zero)."""
+    """The per-linear tickets of the split GEMMs, r4d_gemm_trellis_nt_m64_tickets_bytes(N) (one 128-byte line per
+    128-column group; zeroed once, every complete launch leaves them zero)."""
 
     def __init__(self, N, device="cuda"):
-        self.t = torch.zeros(max(1, N // 128), dtype=torch.int32, device=device)
+        nbytes = lib().r4d_gemm_trellis_nt_m64_tickets_bytes(N)
+        self.t = torch.zeros(max(1, nbytes // 4), dtype=torch.int32, device=device)
 
 
 def _wq_args(wq, K, KB):
@@ -231,6 +232,9 @@ def w4a16_gemm(a, wq, wsz, K, N, group=64, out=None, f32=False, stream=None):
     return out
 
 
+_argmax_streams = set()   # (device, stream) pairs whose argmax scratch the library has allocated
+
+
 def argmax_rows(logits, out_idx=None, out_val=None, stream=None):
     """Per-row argmax of a [rows][vocab] fp32 or bf16 tensor: (int32 [rows], fp32 [rows])."""
     L = lib()
@@ -239,7 +243,14 @@ def argmax_rows(logits, out_idx=None, out_val=None, stream=None):
         out_idx = torch.empty(rows, dtype=torch.int32, device=logits.device)
     if out_val is None:
         out_val = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    if not 1 <= rows <= 64 or vocab < 1:
+        raise ValueError("argmax: rows must be 1..64 and vocab >= 1")
     st = _stream(stream)
+    key = (logits.device.index, st)
+    if key not in _argmax_streams and torch.cuda.is_current_stream_capturing():
+        # the library allocates a stream's argmax scratch at its first call, which graph capture forbids
+        raise ValueError("argmax: the stream's first argmax is under graph capture; run one on it before capturing")
+    _argmax_streams.add(key)
     if logits.dtype == torch.float32:
         L.r4dx_argmax_rows_f32(_p(logits), logits.stride(0), _p(out_idx), _p(out_val), 1, rows, vocab, st)
     elif logits.dtype == torch.bfloat16 and rows == 1:

@@ -328,6 +328,8 @@ __device__ __forceinline__ void r4_store_coherent(float* p, float v) {
 __device__ __forceinline__ float r4_load_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Words per ticket: each 128-column group's counter owns a 128-byte line (the GEMV's ticket layout).
+#define R4_TICKET_WORDS 32
 __device__ __forceinline__ bool r4_ticket_last(unsigned* ticket, unsigned contributors, int* flag_lds) {
   // every coherent store of this thread acknowledged before the barrier (the workgroup-scope fence
   // alone emits no wait on gfx950)

@@ -82,3 +82,9 @@ struct r4d_gemv_args {
   int64_t a2, a3;
   int n_end1, n_end2;
 };
+
+namespace r4d {
+// Checks and launches one trellis GEMV (trellis_gemv.hip); throws std::runtime_error naming `entry` on an illegal
+// launch.
+void gemv_run(r4d_gemv_args& a, const char* entry);
+}  // namespace r4d

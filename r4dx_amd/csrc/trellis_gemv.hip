@@ -419,7 +419,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
           }
         }
     }
-    if (!r4_ticket_last(&tickets[group], (unsigned)(SKG * (4 / NPW)), flag)) return;
+    if (!r4_ticket_last(&tickets[group * R4_TICKET_WORDS], (unsigned)(SKG * (4 / NPW)), flag)) return;
     // Sum the SKG slices: run p (0..7) adds slices p, p + 8, ... in order; the 8 runs are then added
     // in order 0..7 -- the same arithmetic for every element whatever M is. kRedRows rows at a time
     // (bounded LDS); the finished sums land in red[r][128] for the epilogue.
@@ -566,6 +566,26 @@ constexpr size_t kAldsMax = 48 * 1024;   // A slices up to this many bytes are s
 
 constexpr size_t kXfAldsMax = 96 * 1024;   // the fused transform stages the slice in LDS up to this size
 
+// The launch form launch_gemv_np picks: the whole-group form (4 pairs x 1 wave) for the SK = 1 order or an unsplit
+// launch without ws, else the split form (1 pair at M = 1, 2 at M >= 2, each over 4 waves); MT row tiles of 16.
+struct GemvForm {
+  int NPW, SK, MT;
+};
+GemvForm gemv_form(int M, int SKG, bool have_ws, bool sk1) {
+  GemvForm f;
+  f.MT = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  if (sk1 || (SKG == 1 && !have_ws)) { f.NPW = 4; f.SK = 1; }
+  else { f.NPW = M == 1 ? 1 : 2; f.SK = 4; }
+  return f;
+}
+// The LDS bytes of a launch of that form (alds: A staged in LDS, forced by the fused transform).
+size_t gemv_form_lds(int M, int K, int SKG, bool have_ws, bool sk1, bool xf) {
+  const GemvForm f = gemv_form(M, SKG, have_ws, sk1);
+  const int ktw = K / 16 / SKG;
+  const bool alds = xf || gemv_ktl_pad(f.SK, ktw) * M * 32 <= kAldsMax;
+  return gemv_lds(f.MT, f.NPW, f.SK, alds, ktw, M);
+}
+
 template <int KB, int MT, int NPW, int SK, bool ALDS, int XF, bool WQ = false>
 void launch_gemv(const r4d_gemv_args& a) {
   dim3 grid(a.N / 32 / NPW, a.SKG), block(64 * NPW * SK);
@@ -615,14 +635,15 @@ void launch_gemv_a(const r4d_gemv_args& a) {
 // and fewer workgroups take fewer tickets on the group's counter).
 template <int KB, int MT>
 void launch_gemv_np(const r4d_gemv_args& a) {
-  if (a.sk1 || (a.SKG == 1 && (a.ws == 0 || a.tickets == 0))) launch_gemv_a<KB, MT, 4, 1>(a);
-  else if (a.M == 1) launch_gemv_a<KB, MT, 1, 4>(a);
+  const GemvForm f = gemv_form(a.M, a.SKG, a.ws != 0 && a.tickets != 0, a.sk1 != 0);
+  if (f.SK == 1) launch_gemv_a<KB, MT, 4, 1>(a);
+  else if (f.NPW == 1) launch_gemv_a<KB, MT, 1, 4>(a);
   else launch_gemv_a<KB, MT, 2, 4>(a);
 }
 
 template <int KB>
 void launch_gemv_kb(const r4d_gemv_args& a) {
-  const int mt = (a.M + 15) / 16;
+  const int mt = gemv_form(a.M, a.SKG, true, false).MT;
   if (mt <= 1) launch_gemv_np<KB, 1>(a);
   else if (mt <= 2) launch_gemv_np<KB, 2>(a);
   else launch_gemv_np<KB, 4>(a);
@@ -631,6 +652,17 @@ void launch_gemv_kb(const r4d_gemv_args& a) {
 }  // namespace
 
 // ---- host entries ------------------------------------------------------------------------------
+void r4d::gemv_run(r4d_gemv_args& a, const char* entry) {
+  if (!a.a0 || !a.w || !a.c) r4d::fail(entry, "null A, W or C");
+  if (const char* m = r4d_gemm_trellis_nt_m64_check(a.M, a.K, a.N, a.n_split, a.KB, a.SKG, a.full,
+                                                    a.svh != 0, a.ws != 0 && a.tickets != 0))
+    r4d::fail(entry, m);
+  if (a.KB == 4) launch_gemv_kb<4>(a);
+  else if (a.KB == 5) launch_gemv_kb<5>(a);
+  else launch_gemv_kb<3>(a);
+  r4d::launch_ok(entry);
+}
+
 extern "C" {
 
 const char* r4d_gemm_trellis_nt_m64_check(int M, int K, int N, int n_split, int KB, int SKG,
@@ -644,27 +676,19 @@ const char* r4d_gemm_trellis_nt_m64_check(int M, int K, int N, int n_split, int 
   else if (n_split < 0 || n_split > N || n_split % 128) e = "n_split must be in 0..N and a multiple of 128";
   else if (SKG > 1 && !have_ws) e = "SKG > 1 needs ws and tickets";
   else if (full && !have_svh) e = "svh must be non-null";
+  else if ((size_t)SKG * (size_t)M * (size_t)N * 4u > ((size_t)1 << 31))
+    e = "the split partials SKG * M * N * 4 bytes must fit 2 GiB (32-bit offsets of the finish): lower SKG";
   return r4d::check_result(e);
 }
 
-static void tq_run(r4d_gemv_args& a, const char* entry) {
-  if (!a.a0 || !a.w || !a.c) r4d::fail(entry, "null A, W or C");
-  if (const char* m = r4d_gemm_trellis_nt_m64_check(a.M, a.K, a.N, a.n_split, a.KB, a.SKG, a.full,
-                                                    a.svh != 0, a.ws != 0 && a.tickets != 0))
-    r4d::fail(entry, m);
-  if (a.KB == 4) launch_gemv_kb<4>(a);
-  else if (a.KB == 5) launch_gemv_kb<5>(a);
-  else launch_gemv_kb<3>(a);
-  r4d::launch_ok(entry);
-}
 
 void r4d_gemm_trellis_nt_m64(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
                              int64_t ws, int64_t tickets, int M, int K, int N, int KB, int WV, int SK,
                              int MT, int NP, int SKG, int U, int NT, float out_scale, int64_t stream) {
   (void)WV; (void)MT; (void)NP; (void)U; (void)NT;
   r4d_gemv_args a{a0, a1, n_split, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale, stream};
-  a.sk1 = SK == 1;
-  tq_run(a, "gemm_trellis_nt_m64");
+  a.sk1 = SK == 1 || SK == 2;
+  r4d::gemv_run(a, "gemm_trellis_nt_m64");
 }
 
 void r4d_gemm_trellis_nt_m64_raw(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t c, int64_t ws,
@@ -672,9 +696,9 @@ void r4d_gemm_trellis_nt_m64_raw(int64_t a0, int64_t a1, int n_split, int64_t w,
                                  int NP, int SKG, int U, int NT, int64_t clk, int64_t stream) {
   (void)WV; (void)MT; (void)NP; (void)U; (void)NT;
   r4d_gemv_args a{a0, a1, n_split, w, 0, c, ws, tickets, M, K, N, KB, SKG, 0, 1.f, stream};
-  a.sk1 = SK == 1;
+  a.sk1 = SK == 1 || SK == 2;
   a.clk = clk;
-  tq_run(a, "gemm_trellis_nt_m64_raw");
+  r4d::gemv_run(a, "gemm_trellis_nt_m64_raw");
 }
 
 // r4d.h:425-450: the fake-quant measurement entries -- r4d_gemm_trellis_nt_m64 / _raw with every decoded weight
@@ -691,10 +715,10 @@ void r4d_gemm_trellis_nt_m64_wq(int64_t a0, int64_t a1, int n_split, int64_t w, 
   (void)WV; (void)MT; (void)NP; (void)U; (void)NT;
   wq_check(K, KB, wscale, gsh, "gemm_trellis_nt_m64_wq");
   r4d_gemv_args a{a0, a1, n_split, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale, stream};
-  a.sk1 = SK == 1;
+  a.sk1 = SK == 1 || SK == 2;
   a.wsc = wscale;
   a.wq_gsh = gsh;
-  tq_run(a, "gemm_trellis_nt_m64_wq");
+  r4d::gemv_run(a, "gemm_trellis_nt_m64_wq");
 }
 void r4d_gemm_trellis_nt_m64_raw_wq(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t c, int64_t ws,
                                     int64_t tickets, int M, int K, int N, int KB, int WV, int SK, int MT, int NP,
@@ -702,10 +726,10 @@ void r4d_gemm_trellis_nt_m64_raw_wq(int64_t a0, int64_t a1, int n_split, int64_t
   (void)WV; (void)MT; (void)NP; (void)U; (void)NT;
   wq_check(K, KB, wscale, gsh, "gemm_trellis_nt_m64_raw_wq");
   r4d_gemv_args a{a0, a1, n_split, w, 0, c, ws, tickets, M, K, N, KB, SKG, 0, 1.f, stream};
-  a.sk1 = SK == 1;
+  a.sk1 = SK == 1 || SK == 2;
   a.wsc = wscale;
   a.wq_gsh = gsh;
-  tq_run(a, "gemm_trellis_nt_m64_raw_wq");
+  r4d::gemv_run(a, "gemm_trellis_nt_m64_raw_wq");
 }
 // r4d.h:433-436, 441-442
 size_t r4d_trellis_wscale_count(int K, int N, int gsh) {
@@ -750,7 +774,7 @@ void r4dx_gemm_trellis_nt_m64_parts(const int64_t* a, const int* n0, int parts, 
                   out_scale, stream};
   if (parts > 2) { g.a2 = a[2]; g.n_end1 = n0[2]; }
   if (parts > 3) { g.a3 = a[3]; g.n_end2 = n0[3]; }
-  tq_run(g, e);
+  r4d::gemv_run(g, e);
 }
 
 // No reference counterpart: the input transform of r4dx_trellis_input_f16 / _bf16 fused into the GEMV.
@@ -759,8 +783,10 @@ const char* r4dx_trellis_gemv_xf_check(int M, int K, int N, int n_split, int KB,
   std::string e;
   if ((K / 128) % SKG) e = "the fused transform needs whole 128-blocks per slice: (K / 128) % SKG == 0";
   else {
-    const int SK = (SKG == 1 && !have_ws) ? 1 : 4;
-    if (gemv_ktl_pad(SK, K / 16 / SKG) * M * 32 > kXfAldsMax) e = "the A slice does not fit LDS: raise SKG";
+    const GemvForm f = gemv_form(M, SKG, have_ws != 0, false);
+    if (gemv_ktl_pad(f.SK, K / 16 / SKG) * M * 32 > kXfAldsMax) e = "the A slice does not fit LDS: raise SKG";
+    else if (gemv_form_lds(M, K, SKG, have_ws != 0, false, true) > 160 * 1024)
+      e = "the A slice, the split partials and the finish buffers exceed 160 KiB of LDS: lower M or raise SKG";
   }
   return r4d::check_result(e);
 }
@@ -791,7 +817,11 @@ int r4d_gemm_trellis_nt_m64_max_m(void) { return 64; }
 size_t r4d_gemm_trellis_nt_m64_ws_bytes(int M, int N, int SKG) {
   return (size_t)SKG * (size_t)M * (size_t)N * sizeof(float);
 }
-size_t r4d_gemm_trellis_nt_m64_tickets_bytes(int N) { return (size_t)(N > 0 ? N / 128 : 0) * sizeof(unsigned); }
+// One 128-byte line per 128-column group (the counter in its first word): the contributors of different groups
+// then never meet on one cache line's atomics.
+size_t r4d_gemm_trellis_nt_m64_tickets_bytes(int N) {
+  return (size_t)(N > 0 ? N / 128 : 0) * R4_TICKET_WORDS * sizeof(unsigned);
+}
 
 void r4d_gemm_trellis_nt_m64_zero_tickets(int64_t tickets, size_t bytes, int64_t stream) {
   if (bytes == 0) return;
@@ -818,10 +848,11 @@ void r4d_trellis_reconstruct_f16(int64_t w, int64_t q, int K, int N, int KB, int
 }
 
 // This build's split choice for the GEMV, measured on MI355X over the 27B shapes and their same-input merges
-// (KB 4, M = 1 and 8): among the divisors of K/16 (2..32) that leave each of a slice's 4 waves at least 16
-// k-tiles, the ones that launch at least 6 waves per CU are preferred, and of those the one closest to 32
-// k-tiles per wave (log distance; ties to the larger SKG); with none, the largest. E.g. K = 5120: SKG 2 from
-// N = 6144 on (16384 columns: 18.2 us against 20.1 at SKG 4), 5 for N = 1024; K = 6144, N = 5120: 3.
+// (KB 4, M = 1 and 8): among the powers of two 2..8 dividing K/16 (the engine's tuning rows hold no other SKG:
+// TrellisRowFits, src/model/linear.cpp:243-255) that leave each of a slice's 4 waves at least 16 k-tiles, the
+// ones that launch at least 6 waves per CU are preferred, and of those the one closest to 32 k-tiles per wave
+// (log distance; ties to the larger SKG); with none, the largest. E.g. K = 5120: SKG 2 from N = 6144 on
+// (16384 columns: 18.2 us against 20.1 at SKG 4), 4 for N = 1024; K = 6144, N = 5120: 4.
 // Depends on the shape only, so every M <= 16 gets the same row bits.
 int r4d_mi355x_trellis_gemv_skg(int K, int N, int KB) {
   (void)KB;
@@ -835,7 +866,7 @@ int r4d_mi355x_trellis_gemv_skg(int K, int N, int KB) {
   const long long want = 6LL * cus;
   int best = 0, fallback = 1;
   double best_d = 1e30;
-  for (int d = 2; d <= 32 && d <= KT; ++d) {
+  for (int d = 2; d <= 8 && d <= KT; d *= 2) {
     if (KT % d) continue;
     const double per_wave = (double)KT / d / 4.0;
     if (per_wave < 16.0) continue;
@@ -851,3 +882,4 @@ int r4d_mi355x_trellis_gemv_skg(int K, int N, int KB) {
 }
 
 }  // extern "C"
+

@@ -448,19 +448,24 @@ void r4d::launch_split_finish(const float* ws, const float* svh, void* c, int M,
   hipLaunchKernelGGL(tq_m256_finish, dim3(N / 128, M / kFinRows), dim3(256), 0, st, ws, svh, c, M, N, SKG, full, out_scale);
 }
 
+// SK names the M <= 64 row this launch reproduces: 1 or 2 (0 means 1) is r4d_gemm_trellis_nt_m64's one-wave-per-pair
+// order, the only one this kernel computes; 4, 8 and 16 name the 4-wave split order.
+static bool m256_sk_ok(int SK) { return SK == 0 || SK == 1 || SK == 2; }
 static const char* const sk_msg =
-    "SK must be 1 (or 0): the M <= 64 row this reproduces is r4d_gemm_trellis_nt_m64's SK = 1 form";
+    "SK must be 1 or 2 (0 means 1): the M <= 64 row this reproduces is r4d_gemm_trellis_nt_m64's one-wave-per-pair "
+    "order (its SK 1 and 2); SK 4, 8 and 16 name the 4-wave split order, which this kernel does not compute";
 
 extern "C" {
 
 // r4d.h:416-419. Every element equals, bit for bit, what r4d_gemm_trellis_nt_m64 gives it at M = 64 with
-// SK = 1 and the same SKG (the same MFMA operands in the same order per K slice, the same slice order and
-// epilogue). SK must be 0 or 1 (0 means 1); NP, U and skw are the reference's geometry knobs: accepted, unused.
+// SK = 1 (or 2: the same order) and the same SKG (the same MFMA operands in the same order per K slice, the same
+// slice order and epilogue). SK must be 0, 1 or 2 (0 means 1); NP, U and skw are the reference's geometry knobs:
+// accepted, unused.
 void r4d_gemm_trellis_nt_m256(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
                               int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SK, int NP,
                               int SKG, int U, float out_scale, int64_t stream, int skw) {
   (void)NP; (void)U; (void)skw;
-  if (SK != 0 && SK != 1) r4d::fail("gemm_trellis_nt_m256", sk_msg);
+  if (!m256_sk_ok(SK)) r4d::fail("gemm_trellis_nt_m256", sk_msg);
   m256_run(a0, a1, n_split, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale, stream,
            "gemm_trellis_nt_m256");
 }
@@ -468,7 +473,7 @@ void r4d_gemm_trellis_nt_m256(int64_t a0, int64_t a1, int n_split, int64_t w, in
 const char* r4d_gemm_trellis_nt_m256_check(int M, int K, int N, int n_split, int KB, int SK, int NP, int SKG,
                                            int U, int skw) {
   (void)NP; (void)U; (void)skw;
-  if (SK != 0 && SK != 1) return r4d::check_result(sk_msg);
+  if (!m256_sk_ok(SK)) return r4d::check_result(sk_msg);
   return r4d::check_result(m256_check(M, K, N, n_split, KB, SKG));
 }
 
@@ -505,14 +510,14 @@ void r4d_gemm_trellis_nt_m256_raw(int64_t a0, int64_t a1, int n_split, int64_t w
 
 // r4d.h:451-454: r4d_gemm_trellis_nt_m256 with the weight fake-quant of the _wq entries (the scale table of
 // r4d_trellis_wscale_f32, 2^gsh k-tiles per group; a null table throws). Bit-identical, per element, to
-// r4d_gemm_trellis_nt_m64_wq at M = 64, SK = 1 and the same SKG.
+// r4d_gemm_trellis_nt_m64_wq at M = 64, SK = 1 (or 2) and the same SKG.
 void r4d_gemm_trellis_nt_m256_wq(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
                                  int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SK, int NP,
                                  int SKG, int U, float out_scale, int64_t stream, int skw, int64_t wscale,
                                  int gsh) {
   (void)NP; (void)U; (void)skw;
   const char* e = "gemm_trellis_nt_m256_wq";
-  if (SK != 0 && SK != 1) r4d::fail(e, sk_msg);
+  if (!m256_sk_ok(SK)) r4d::fail(e, sk_msg);
   if (!wscale) r4d::fail(e, "the _wq entry needs a scale table (r4d_trellis_wscale_f32)");
   if (gsh < 1 || gsh > 3 || K % (16 << gsh)) r4d::fail(e, "gsh must be 1, 2 or 3 with 16 << gsh dividing K");
   if (KB != 4 && KB != 5) r4d::fail(e, "KB must be 4 or 5");
@@ -521,7 +526,9 @@ void r4d_gemm_trellis_nt_m256_wq(int64_t a0, int64_t a1, int n_split, int64_t w,
 
 // This build's K split for the prefill GEMM: the workgroup count per CU decides the critical path
 // (one resident per CU: the two LDS stages take 96 KiB), so SKG minimises ceil(G SKG / CUs) x steps
-// per slice plus the cost of the second pass (SKG x M x N fp32 written and read back).
+// per slice plus the cost of the second pass (SKG x M x N fp32 written and read back). SKG is a power of two
+// up to 8: the engine's tuning rows hold no other (TrellisRowFits, src/model/linear.cpp:243-255), and the M = 64
+// band's row carries this SKG (PlanTrellisM256 reads it there, linear.cpp:696-701).
 int r4d_mi355x_trellis_m256_skg(int K, int N, int KB) {
   (void)KB;
   const int KT = K / 16, G = N / 128;
@@ -533,7 +540,7 @@ int r4d_mi355x_trellis_m256_skg(int K, int N, int KB) {
   }
   int best = 1;
   double best_cost = 1e30;
-  for (int d = 1; d <= 16; ++d) {
+  for (int d = 1; d <= 8; d *= 2) {
     if (KT % (4 * d)) continue;
     const double rounds = (double)(((long long)G * d + cus - 1) / cus);
     const double steps = (double)KT / (4 * d);

@@ -38,6 +38,9 @@
 #include "r4d_host.h"
 #include "r4d_mi355x.h"
 
+#include <map>
+#include <mutex>
+
 namespace {
 
 typedef __amdgpu_buffer_rsrc_t r4_rsrc;
@@ -367,49 +370,95 @@ __device__ __forceinline__ unsigned long long am_wave_max(unsigned long long k) 
   return k;
 }
 
-constexpr int kAmParts = 128;         // partial keys per row (first pass workgroups per row)
+constexpr int kAmParts = 256;         // most workgroups per row (partial keys per row)
 constexpr int kAmMaxRows = 64;
-// Library-owned partials of the two-pass argmax: each row's kAmParts keys. Every call on a device
-// shares it (calls that overlap on one device race; stream-ordered calls do not).
-__device__ unsigned long long g_am_part[kAmMaxRows * kAmParts];
+constexpr int kAmPerThread = 8;       // elements per thread and batch: all 8 loads issued before any compare
+constexpr int kAmThreads = 256;
 
+// Partial keys of one argmax: [kAmMaxRows][kAmParts] u64, then a ticket line (R4_TICKET_WORDS u32) per row. Each
+// row's workgroups store their keys, take the row's ticket, and the last one reduces the row and resets the ticket.
+struct AmScratch {
+  unsigned long long* keys;
+  unsigned* tickets;
+};
+constexpr size_t kAmScratchBytes =
+    (size_t)kAmMaxRows * kAmParts * sizeof(unsigned long long) + (size_t)kAmMaxRows * R4_TICKET_WORDS * sizeof(unsigned);
+
+// One launch: workgroup (b, row) reduces elements [b chunk, (b + 1) chunk) of its row to one key; the last of the
+// row's nblk workgroups (ticket) reduces their keys in a fixed order and writes the result.
 template <bool BF16>
-__global__ __launch_bounds__(256) void am_pass1(const void* __restrict__ x, long long row_stride, long long vocab) {
+__global__ __launch_bounds__(kAmThreads) void am_kernel(const void* __restrict__ x, long long row_stride,
+                                                        long long vocab, long long chunk, int nblk, AmScratch sc,
+                                                        int* __restrict__ out_idx, float* __restrict__ out_val,
+                                                        long long out_stride) {
   const int row = blockIdx.y;
-  const long long chunk = (vocab + kAmParts - 1) / kAmParts;
   const long long b = (long long)blockIdx.x * chunk, e = b + chunk < vocab ? b + chunk : vocab;
+  const long long base = (long long)row * row_stride;
   unsigned long long k = 0;
-  for (long long i = b + threadIdx.x; i < e; i += 256) {
-    const float v = BF16 ? r4_bf16_to_f32(((const unsigned short*)x)[row * row_stride + i])
-                         : ((const float*)x)[row * row_stride + i];
-    k = am_max(k, am_key(v, (unsigned)i));
+  for (long long i0 = b + threadIdx.x; i0 < e; i0 += (long long)kAmThreads * kAmPerThread) {
+    float v[kAmPerThread];
+#pragma unroll
+    for (int u = 0; u < kAmPerThread; ++u) {
+      const long long i = i0 + (long long)u * kAmThreads;
+      v[u] = __builtin_nanf("");
+      if (i < e) v[u] = BF16 ? r4_bf16_to_f32(((const unsigned short*)x)[base + i]) : ((const float*)x)[base + i];
+    }
+#pragma unroll
+    for (int u = 0; u < kAmPerThread; ++u) k = am_max(k, am_key(v[u], (unsigned)(i0 + (long long)u * kAmThreads)));
   }
-  __shared__ unsigned long long red[4];
+  __shared__ unsigned long long red[kAmThreads / 64];
+  __shared__ int flag;
   k = am_wave_max(k);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = k;
   __syncthreads();
-  if (threadIdx.x == 0) g_am_part[row * kAmParts + blockIdx.x] = am_max(am_max(red[0], red[1]), am_max(red[2], red[3]));
-}
-
-template <bool BF16>
-__global__ __launch_bounds__(64) void am_pass2(const void* __restrict__ x, long long row_stride,
-                                               int* __restrict__ out_idx, float* __restrict__ out_val,
-                                               long long out_stride) {
-  const int row = blockIdx.x;
-  unsigned long long k = 0;
-  for (int i = threadIdx.x; i < kAmParts; i += 64) k = am_max(k, g_am_part[row * kAmParts + i]);
-  k = am_wave_max(k);
+  if (threadIdx.x == 0) {
+    const unsigned long long kb = am_max(am_max(red[0], red[1]), am_max(red[2], red[3]));
+    __hip_atomic_store(&sc.keys[row * kAmParts + blockIdx.x], kb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!r4_ticket_last(&sc.tickets[row * R4_TICKET_WORDS], (unsigned)nblk, &flag)) return;
+  if (threadIdx.x >= 64) return;
+  unsigned long long kr = 0;
+  for (int i = threadIdx.x; i < nblk; i += 64)
+    kr = am_max(kr, __hip_atomic_load(&sc.keys[row * kAmParts + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  kr = am_wave_max(kr);
   if (threadIdx.x == 0) {
     int idx;
     float val;
-    am_decode(k, &idx, &val);
+    am_decode(kr, &idx, &val);
     out_idx[row * out_stride] = idx;
     // the winner's own bits (a -0 stays -0); the seed's value when nothing beat it
     if (out_val)
-      out_val[row * out_stride] = k < am_key(-__builtin_inff(), 0u) ? val
-                                  : BF16 ? r4_bf16_to_f32(((const unsigned short*)x)[row * row_stride + idx])
-                                         : ((const float*)x)[row * row_stride + idx];
+      out_val[row * out_stride] = kr < am_key(-__builtin_inff(), 0u) ? val
+                                  : BF16 ? r4_bf16_to_f32(((const unsigned short*)x)[base + idx])
+                                         : ((const float*)x)[base + idx];
   }
+}
+
+// The scratch of one (device, stream): allocated and zeroed at the stream's first argmax, kept for the process
+// (the reference keeps its argmax partials per stream the same way, src/kernels/src/r4dx_kernels.hip:1715-1734),
+// so argmax calls on different streams of one device -- an MTP head beside its model -- never share partials.
+// A first call on a stream under graph capture cannot allocate and throws: run one argmax on that stream first.
+AmScratch am_scratch(hipStream_t st, const char* entry) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, void*> by_stream;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) r4d::fail(entry, "no current device");
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = by_stream.find({dev, st});
+  if (it == by_stream.end()) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      r4d::fail(entry, "the stream's first argmax is under graph capture, where its scratch cannot be allocated: "
+                       "run one argmax on this stream before capturing");
+    void* p = nullptr;
+    if (hipMalloc(&p, kAmScratchBytes) != hipSuccess) r4d::fail(entry, "scratch allocation failed");
+    if (hipMemset(p, 0, kAmScratchBytes) != hipSuccess) r4d::fail(entry, "scratch clear failed");
+    it = by_stream.emplace(std::make_pair(dev, st), p).first;
+  }
+  AmScratch s;
+  s.keys = (unsigned long long*)it->second;
+  s.tickets = (unsigned*)(s.keys + (size_t)kAmMaxRows * kAmParts);
+  return s;
 }
 
 void am_run(bool bf16, int64_t x, int64_t row_stride, int64_t out_idx, int64_t out_val, int64_t out_stride,
@@ -418,14 +467,20 @@ void am_run(bool bf16, int64_t x, int64_t row_stride, int64_t out_idx, int64_t o
   if (vocab < 1 || vocab > 0x7FFFFFFFLL) r4d::fail(entry, "vocab must be 1..2^31-1");
   if (!x || !out_idx) r4d::fail(entry, "null buffer");
   hipStream_t st = (hipStream_t)stream;
-  if (bf16) hipLaunchKernelGGL(am_pass1<true>, dim3(kAmParts, (unsigned)rows), dim3(256), 0, st, (const void*)x,
-                               (long long)row_stride, (long long)vocab);
-  else hipLaunchKernelGGL(am_pass1<false>, dim3(kAmParts, (unsigned)rows), dim3(256), 0, st, (const void*)x,
-                          (long long)row_stride, (long long)vocab);
-  if (bf16) hipLaunchKernelGGL(am_pass2<true>, dim3((unsigned)rows), dim3(64), 0, st, (const void*)x,
-                               (long long)row_stride, (int*)out_idx, (float*)out_val, (long long)out_stride);
-  else hipLaunchKernelGGL(am_pass2<false>, dim3((unsigned)rows), dim3(64), 0, st, (const void*)x,
-                          (long long)row_stride, (int*)out_idx, (float*)out_val, (long long)out_stride);
+  const AmScratch sc = am_scratch(st, entry);
+  // one batch of kAmPerThread elements per thread and workgroup where kAmParts workgroups allow it
+  const long long per = (long long)kAmThreads * kAmPerThread;
+  long long nblk = (vocab + per - 1) / per;
+  if (nblk > kAmParts) nblk = kAmParts;
+  const long long chunk = (vocab + nblk - 1) / nblk;
+  nblk = (vocab + chunk - 1) / chunk;
+  const dim3 grid((unsigned)nblk, (unsigned)rows);
+  if (bf16) hipLaunchKernelGGL(am_kernel<true>, grid, dim3(kAmThreads), 0, st, (const void*)x, (long long)row_stride,
+                               (long long)vocab, chunk, (int)nblk, sc, (int*)out_idx, (float*)out_val,
+                               (long long)out_stride);
+  else hipLaunchKernelGGL(am_kernel<false>, grid, dim3(kAmThreads), 0, st, (const void*)x, (long long)row_stride,
+                          (long long)vocab, chunk, (int)nblk, sc, (int*)out_idx, (float*)out_val,
+                          (long long)out_stride);
   r4d::launch_ok(entry);
 }
 

@@ -6,8 +6,12 @@ contract:
 
 * every M <= 16 gets the same (SK, SKG), so a verify row's bits equal the decode row's (the row-identity rule,
   src/model/linear.cpp:33-53);
-* the M = 64 band's row is (SK = 1, SKG of the M = 256 plan), the order r4d_gemm_trellis_nt_m256 reproduces bit
-  for bit, so an M = 256 chunk and four M = 64 chunks of the same rows agree;
+* the M = 64 band's row is (SK = 2, SKG of the M = 256 plan): SK 1 and 2 both name the one-wave-per-pair order
+  r4d_gemm_trellis_nt_m256 reproduces bit for bit, so an M = 256 chunk and four M = 64 chunks of the same rows
+  agree, and SK = 2 lets the engine's PlanTrellisM256 (src/model/linear.cpp:705-722, skw <= SK, skw from
+  {2, 4, 8}) find its K-slice grouping;
+* every SKG is a power of two up to 8, the only values the engine's tuning rows may hold (TrellisRowFits,
+  src/model/linear.cpp:243-255);
 * a plan is refused, with the reason, when the shape breaks the loader's rules (KB 4 or 5 for the prefill
   kernels, 1 or 2 parts, whole 128-blocks, a part boundary inside N) or the kernel's own `_check` refuses it --
   so a plan never names a launch that would throw.
@@ -26,7 +30,7 @@ class Plan:
     ok: bool
     why: str = ""
     kernel: str = ""   # "m64" (r4d_gemm_trellis_nt_m64), "m256", "i8" / "i8c"
-    SK: int = 0        # m64: 1 = one wave per tile pair over its slice, 4 = four waves in k order
+    SK: int = 0        # m64: 1 or 2 = one wave per tile pair over its slice, 4 = four waves in k order
     SKG: int = 1       # K slices across the grid
     skw: int = 0       # int8: the caller's skw argument (checked, not a kernel knob here)
 
@@ -59,7 +63,7 @@ def linear_tuning(N, K, kb, M, parts=1, part_n0=None):
     if M <= DECODE_M:
         SK, SKG = 4, int(lib().r4d_mi355x_trellis_gemv_skg(K, N, kb))
     else:
-        SK, SKG = 1, m256_skg(N, K, kb)
+        SK, SKG = 2, m256_skg(N, K, kb)
     n_split = part_n0 if parts == 2 else N
     msg = lib().r4d_gemm_trellis_nt_m64_check(M, K, N, n_split, kb, SKG, 1, 1, 1)
     if msg:
@@ -68,16 +72,17 @@ def linear_tuning(N, K, kb, M, parts=1, part_n0=None):
 
 
 def plan_trellis_m256(N, K, kb, parts=1, part_n0=None, M=PREFILL_M):
-    """PlanTrellisM256 (linear.cpp:680-722): SK = 1 and the SKG the M = 64 band uses."""
+    """PlanTrellisM256 (linear.cpp:680-722): the M = 64 band's (SK = 2, SKG), skw = 2 (the first of the engine's
+    preference order {2, 4, 8, 2} not above SK)."""
     why = _shape_why(N, K, kb, parts, part_n0 or 0, rates=(4, 5))
     if why:
         return Plan(False, why)
     skg = m256_skg(N, K, kb)
     n_split = part_n0 if parts == 2 else N
-    msg = lib().r4d_gemm_trellis_nt_m256_check(M, K, N, n_split, kb, 1, 1, skg, 4, 0)
+    msg = lib().r4d_gemm_trellis_nt_m256_check(M, K, N, n_split, kb, 2, 1, skg, 4, 2)
     if msg:
         return Plan(False, msg.decode())
-    return Plan(True, "", "m256", 1, skg)
+    return Plan(True, "", "m256", 2, skg, 2)
 
 
 def plan_trellis_i8(N, K, kb, parts=1, part_n0=None, coarse=False):

@@ -34,11 +34,45 @@ def test_gemv_checks(L):
     assert b"svh" in ck(1, 5120, 5120, 5120, 4, 1, 1, 0, 1)
     assert b"n_split" in ck(1, 5120, 5120, 100, 4, 1, 1, 1, 1)
     assert ck(1, 5120, 5120, 5120, 4, 1, 0, 0, 0) is None      # _raw needs no svh
+    # the finish addresses the partials with 32-bit offsets: SKG M N 4 must fit 2 GiB
+    assert ck(64, 5120, 262144, 262144, 4, 32, 1, 1, 1) is None
+    assert b"2 GiB" in ck(64, 5120, 262144 + 128, 262144 + 128, 4, 32, 1, 1, 1)
+
+
+def test_xf_check_bounds_the_whole_lds():
+    """r4dx_trellis_gemv_xf_check refuses every launch whose LDS request (A slice + the split form's partial
+    accumulators + the finish's buffers) exceeds 160 KiB -- e.g. M = 64, K = 5120, SKG = 8 with ws, which the A
+    slice alone (96 KiB) would let through -- so the entry never throws on a shape the check accepts. Every
+    accepted (M, SKG) is reproduced by the same sizing rule here."""
+    L = loader.lib()
+    ck = L.r4dx_trellis_gemv_xf_check
+    assert b"160 KiB" in ck(64, 5120, 5120, 5120, 4, 8, 1)
+    assert b"160 KiB" in ck(48, 5120, 5120, 5120, 4, 8, 1)
+
+    def lds(M, K, SKG, ws):
+        split = ws or SKG > 1
+        npw, sk = (1 if M == 1 else 2, 4) if split else (4, 1)
+        mt = 1 if M <= 16 else 2 if M <= 32 else 4
+        ktw = K // 16 // SKG
+        steps = (ktw + 3) // 4
+        pad = sk * ((steps + sk - 1) // sk) * 4
+        return pad * M * 32 + 32 + (sk - 1) * npw * 8 * mt * 64 * 4 + (M + 8 * min(M, 4)) * 128 * 4 + 16, pad * M * 32
+
+    for K in (1024, 5120, 6144, 17408):
+        for SKG in (1, 2, 4, 8, 10, 16, 34, 40):
+            if (K // 128) % SKG:
+                continue
+            for M in range(1, 65):
+                for ws in (0, 1):
+                    total, a_bytes = lds(M, K, SKG, ws)
+                    ok = ck(M, K, 1024, 1024, 4, SKG, ws) is None
+                    want = (ws or SKG == 1) and a_bytes <= 96 * 1024 and total <= 160 * 1024
+                    assert ok == want, (K, SKG, M, ws)
 
 
 def test_sizes_and_rates(L):
     assert L.r4d_gemm_trellis_nt_m64_ws_bytes(8, 5120, 4) == 4 * 8 * 5120 * 4
-    assert L.r4d_gemm_trellis_nt_m64_tickets_bytes(5120) == 40 * 4
+    assert L.r4d_gemm_trellis_nt_m64_tickets_bytes(5120) == 40 * 128   # one 128-byte line per group
     assert L.r4d_gemm_trellis_nt_m64_max_m() == 64
     assert [L.r4d_gemm_trellis_nt_m64_has_rate(k) for k in (2, 3, 4, 5, 6)] == [0, 1, 1, 1, 0]
 
@@ -55,6 +89,10 @@ def test_m256_checks(L):
     assert ck(128, 5120, 5120, 5120, 5, 0, 0, 1, 0, 0) is None
     assert b"M must be" in ck(64, 5120, 5120, 5120, 4, 0, 0, 1, 0, 0)
     assert b"SKG" in ck(256, 5120, 5120, 5120, 4, 0, 0, 3, 0, 0)
+    # SK 1 and 2 name the M = 64 one-wave-per-pair order this kernel reproduces; 4, 8, 16 the split order
+    assert ck(256, 5120, 5120, 5120, 4, 2, 1, 2, 4, 2) is None and ck(256, 5120, 5120, 5120, 4, 1, 1, 2, 4, 0) is None
+    for sk in (4, 8, 16):
+        assert b"SK must be 1 or 2" in ck(256, 5120, 5120, 5120, 4, sk, 1, 2, 4, 4)
     assert L.r4d_gemm_trellis_nt_m256_ws_bytes(256, 5120, 2) == 2 * 256 * 5120 * 4
     for K, N in [(5120, 17408), (17408, 5120), (5120, 1024), (6144, 5120)]:
         skg = L.r4d_mi355x_trellis_m256_skg(K, N, 4)

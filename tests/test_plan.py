@@ -1,5 +1,5 @@
 """The MI355X tuning plan (r4dx_amd/plan.py): refusals with a reason (the rules of src/model/linear.cpp:680-766),
-the row-identity rule (every M <= 16 the same knobs), the M = 64 band on the M = 256 plan's (SK = 1, SKG), and
+the row-identity rule (every M <= 16 the same knobs), the M = 64 band on the M = 256 plan's (SK = 2, SKG), and
 every accepted plan legal by the kernels' own _check. CPU only (the planners and checks launch nothing); the
 GPU identity of an M = 256 launch with the M = 64 band's rows is tests/test_m256_gpu.py's."""
 import pytest
@@ -17,7 +17,7 @@ def test_plans_of_the_config1_shapes(N, K, kb):
     assert all(p.ok for p in decode) and len({(p.SK, p.SKG) for p in decode}) == 1
     band = [plan.linear_tuning(N, K, kb, M) for M in (17, 32, 33, 64)]
     m256 = plan.plan_trellis_m256(N, K, kb)
-    assert m256.ok and all(p.ok and (p.SK, p.SKG) == (1, m256.SKG) for p in band)
+    assert m256.ok and all(p.ok and (p.SK, p.SKG) == (2, m256.SKG) for p in band)
     i8 = plan.plan_trellis_i8(N, K, kb)
     assert i8.ok and i8.skw in (2, 4, 8) and (K // 128) % (i8.skw * i8.SKG) == 0
 
@@ -64,15 +64,16 @@ def test_plans_of_the_tp2_rank_shapes(N, K, parts, n0, kb):
 @pytest.mark.parametrize("K,N", [(5120, 16384), (5120, 8192), (5120, 34816), (6144, 5120), (17408, 5120),
                                  (5120, 1024), (1024, 512), (8704, 5120), (3072, 5120)])
 def test_gemv_split_planner_rules(K, N):
-    """r4d_mi355x_trellis_gemv_skg: a divisor of K/16 (whole k-tiles per slice), at least 16 k-tiles per wave of a
-    slice when any split allows it, and the documented picks on the step's launch shapes."""
+    """r4d_mi355x_trellis_gemv_skg: a power of two up to 8 dividing K/16 (whole k-tiles per slice; the engine's rows
+    hold no other SKG), at least 16 k-tiles per wave of a slice when any split allows it, and the documented picks on
+    the step's launch shapes."""
     from r4dx_amd import api
     skg = api.trellis_gemv_skg(K, N, 4)
     KT = K // 16
-    assert KT % skg == 0
+    assert KT % skg == 0 and skg in (1, 2, 4, 8)
     if skg > 1:
         assert KT / skg / 4 >= 16
-    want = {(5120, 16384): 2, (5120, 8192): 2, (5120, 34816): 2, (6144, 5120): 3, (17408, 5120): 8,
-            (5120, 1024): 5, (1024, 512): 1}
+    want = {(5120, 16384): 2, (5120, 8192): 2, (5120, 34816): 2, (6144, 5120): 4, (17408, 5120): 8,
+            (5120, 1024): 4, (1024, 512): 1}
     if (K, N) in want:
         assert skg == want[(K, N)]

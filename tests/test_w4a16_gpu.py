@@ -164,3 +164,43 @@ def test_argmax_order_cases():
     wid = row.float().cpu().numpy()
     v = C.c_float()
     assert int(i_b[0]) == O.lib().r4o_argmax_f32(ptr(wid), wid.shape[0], C.byref(v))
+
+
+def test_argmax_two_streams_and_long_rows():
+    """Two argmax calls in flight on two streams of one device, on different rows, each against the oracle
+    (every stream has its own partials and tickets); a vocab of 2 000 003 (more than one batch of 8 elements
+    per thread in each of the 256 workgroups of a row) with its maximum in the last element, at 64 rows; and
+    100 calls in a row on one stream (the tickets self-reset) giving the same answer each time."""
+    banner("argmax streams")
+    rng = np.random.default_rng(11)
+    xa = rng.standard_normal((5, 248320)).astype(np.float32)
+    xb = rng.standard_normal((7, 248320)).astype(np.float32)
+    da, db = dev(xa), dev(xb)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for s in (s1, s2):   # the first call on each stream allocates its scratch
+        with torch.cuda.stream(s):
+            api.argmax_rows(da[:1])
+    torch.cuda.synchronize()
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            ia, va = api.argmax_rows(da)
+        with torch.cuda.stream(s2):
+            ib, vb = api.argmax_rows(db)
+        torch.cuda.synchronize()
+        for x, idx in ((xa, ia), (xb, ib)):
+            for m in range(x.shape[0]):
+                v = C.c_float()
+                assert int(idx[m]) == O.lib().r4o_argmax_f32(ptr(x[m]), x.shape[1], C.byref(v))
+    big = rng.standard_normal((64, 2000003)).astype(np.float32)
+    big[:, -1] = 50.0
+    big[3, 5] = 50.0   # a tie: the lower index wins
+    idx, _ = api.argmax_rows(dev(big))
+    torch.cuda.synchronize()
+    want = np.full(64, 2000002)
+    want[3] = 5
+    assert np.array_equal(idx.cpu().numpy(), want)
+    first = api.argmax_rows(da)[0].cpu().numpy()
+    for _ in range(100):
+        i, _v = api.argmax_rows(da)
+    torch.cuda.synchronize()
+    assert np.array_equal(i.cpu().numpy(), first)
