@@ -63,6 +63,18 @@ void r4dx_trellis_gemv_xf(int64_t x, int x_is_bf16, int64_t suh0, int64_t suh1, 
                           int SKG, float out_scale, int64_t stream);
 const char* r4dx_trellis_gemv_xf_check(int M, int K, int N, int n_split, int KB, int SKG, int have_ws);
 
+/* No reference counterpart: for callers that cannot allocate or hold a workspace (code under HIP graph capture,
+ * serving loops that forbid hipMalloc). r4d_gemm_trellis_nt_m64 (same C, A parts, SK and SKG meaning) with no ws or
+ * tickets argument: the split partials and tickets live in a device array the library holds per GPU until the
+ * process ends (16 MiB of partials -- SKG M N 4 bytes at most, r4dx_gemm_trellis_nt_m64_noalloc_max_ws_bytes() --
+ * and tickets for N up to 262144). Nothing is allocated on any call. Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU race. The _check form returns NULL or the rule a launch breaks (sizes beyond the
+ * array included); the entry throws on the same. */
+void r4dx_gemm_trellis_nt_m64_noalloc(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c, int M,
+                                      int K, int N, int KB, int SK, int SKG, float out_scale, int64_t stream);
+const char* r4dx_gemm_trellis_nt_m64_noalloc_check(int M, int K, int N, int n_split, int KB, int SKG);
+size_t r4dx_gemm_trellis_nt_m64_noalloc_max_ws_bytes(void);
+
 /* ---- trellis prefill GEMM, M = 128 or 256 ------------------------------------------------------ */
 /* r4d.h:416-419 r4d_gemm_trellis_nt_m256: the linear of r4d_gemm_trellis_nt_m64 for 128 or 256 rows
  * (two launches when SKG > 1: the slices, then their sum and the epilogue); ws fp32 ws_bytes(M, N,

@@ -83,6 +83,9 @@ SIGS = {
     "r4dx_attn_gate_mul_trellis_i8r": (None, [I64] * 7 + [I32, I64]),
     "r4dx_silu_mul_wide_bf16": (None, [I64] * 6),
     "r4dx_model_attn_gate_mul_bf16": (None, [I64] * 5),
+    "r4dx_gemm_trellis_nt_m64_noalloc": (None, [I64, I64, I32, I64, I64, I64] + [I32] * 6 + [F32, I64]),
+    "r4dx_gemm_trellis_nt_m64_noalloc_check": (CSTR, [I32] * 6),
+    "r4dx_gemm_trellis_nt_m64_noalloc_max_ws_bytes": (SZ, []),
 }
 
 _lib = None
