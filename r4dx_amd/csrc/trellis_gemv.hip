@@ -99,7 +99,9 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     float* __restrict__ ws, unsigned* __restrict__ tickets, int M, int K, int N, int SKG, int full,
     float out_scale, const float* __restrict__ suh0, const float* __restrict__ suh1, float xscale,
     unsigned long long* __restrict__ clk, const float* __restrict__ wsc, int wq_gsh) {
-  constexpr int PF = 4;
+  // steps in flight; 2 where each ring slot also carries MT row tiles of A from global memory (4 slots of 4 row
+  // tiles would not fit the VGPRs and spill)
+  constexpr int PF = (!ALDS && MT >= 4) ? 2 : 4;
   constexpr int NT = 64 * NPW * SK;
   constexpr int NW = NPW * SK;                 // waves
   constexpr int BLK = 16 * KB;                 // words per (pair, k-tile) block

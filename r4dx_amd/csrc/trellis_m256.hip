@@ -155,10 +155,15 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
         load(ring[(i + 1) % PF], st + i + 1 + PF);
       }
     }
+    static_assert(PF == 2, "the tail below names the two ring slots");
     for (; st < nst; ++st) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
-      if (st + 1 < nst) put(ring[(st + 1) % PF == 0 ? 0 : 1], st + 1);
+      // ring slots are named by constants only: a runtime index would move the whole ring to scratch memory
+      if (st + 1 < nst) {
+        if (((st + 1) & 1) == 0) put(ring[0], st + 1);
+        else put(ring[1], st + 1);
+      }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (SKG == 1 && full) {      // the epilogue's two exchange rounds
