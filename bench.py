@@ -35,6 +35,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-only", action="store_true", help="only the GEMV launches (for rocprof)")
     ap.add_argument("--no-m256", action="store_true", help="skip the M = 256 prefill GEMM leg")
+    ap.add_argument("--no-rows", action="store_true", help="skip the config-1 rows at M 2/4/8, KB 5 and the mix")
     ap.add_argument("--no-w4", action="store_true", help="skip the w4a16 LM-head leg")
     ap.add_argument("--no-i8", action="store_true", help="skip the int8 prefill GEMM legs")
     ap.add_argument("--pmc-prefill", action="store_true",
@@ -218,6 +219,11 @@ def main():
     u1.record(stream)
     torch.cuda.synchronize()
     ms_step_fused = u0.elapsed_time(u1) / copies
+    # the same layer as 6 fused launches (r4dx_trellis_gemv_xf_parts: each group's transform inside its GEMV)
+    fl, fcopies, _ = config1_layer(api, WL, M, lambda g: KB, gen)
+    _, fused_parts = config1_steps(api, fl, fcopies, out_scale)
+    ms_step_fparts = _graph_ms(lambda: [fused_parts(c) for c in range(fcopies)], max(1, reps), fcopies)
+    del fl
     # the reference engine's launch pattern: one GEMV per projection (9 launches)
     g_proj = capture(lambda: [step(c) for c in range(copies)])
     g_proj.replay()
@@ -255,6 +261,7 @@ def main():
             per_proj[L["name"]] = rec
     achieved = alg_bytes / (gemv_ms * 1e-3) / 1e9
 
+    rows = None if args.no_rows else bench_config1_rows(api, WL)
     m256 = None if args.no_m256 else bench_m256(api, WL, KB)
     w4 = None if args.no_w4 else bench_w4a16(api, WL)
     i8 = None if args.no_i8 else bench_int8(api, WL)
@@ -292,7 +299,12 @@ def main():
                    "per_projection_launch_GBs": per_proj,
                    "fused_xf_ms_per_step": round(ms_step_fused, 4),
                    "fused_xf_GBs": round(layer_wbytes / (ms_step_fused * 1e-3) / 1e9, 1),
-                   "fused_xf_step": "9 r4dx_trellis_gemv_xf launches (transform inside the GEMV), per projection"},
+                   "fused_xf_step": "9 r4dx_trellis_gemv_xf launches (transform inside the GEMV), per projection",
+                   "fused_parts_ms_per_step": round(ms_step_fparts, 4),
+                   "fused_parts_GBs": round(layer_wbytes / (ms_step_fparts * 1e-3) / 1e9, 1),
+                   "fused_parts_step": "6 r4dx_trellis_gemv_xf_parts launches (each group's input transform inside "
+                                       "its GEMV)",
+                   "rows": rows},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic("tq_gemv_kernel", KB, M, [L["name"] for L in merged]),
                      "kernel": "tq_gemv_kernel", "avg_launch_us": round(gemv_ms * 1e3 / len(merged), 3),
@@ -305,6 +317,97 @@ def main():
         "wall_s": round(wall, 3),
     }
     print(json.dumps(line), flush=True)
+
+
+# The 4/5-bit mix of the config-1 rows: the GDN and attention projections at KB 5, the MLP at KB 4 (4.41 bits per
+# weight over the layer's weights; the reference reports its 4.5 bpw mix beside K4, docs/trellis-kernel.md:1380-1388).
+MIX_KB5 = ("gdn.in", "gdn.out", "attn.in", "attn.o")
+
+
+def config1_layer(api, WL, M, kb_of, gen, min_bytes=1 << 30):
+    """One layer of config 1 at M rows, group g's linears at KB kb_of(g): the 6 launch groups (the projections that
+    share an input laid out as one linear), each with >= min_bytes of rotating weight copies over the layer.
+    Returns (launch list, copies, weight bytes per step)."""
+    import numpy as np
+    import torch
+    dev = torch.device("cuda:0")
+    shape = {name: (K, N) for name, K, N in WL.LAYER_SHAPES}
+    wbytes = 0
+    specs = []
+    for gi, (gname, members) in enumerate(WL.LAYER_GROUPS):
+        KB = kb_of(gname)
+        K = shape[members[0][0]][0]
+        widths = [shape[p][1] for lin in members for p in lin]
+        N = sum(widths)
+        wbytes += K * N * KB // 8
+        specs.append((gi, gname, KB, K, N, widths))
+    copies = max(2, int(np.ceil(min_bytes / wbytes)) + 1)
+    layer = []
+    for gi, gname, KB, K, N, widths in specs:
+        nw = K * N * KB // 32
+        skg = api.trellis_gemv_skg(K, N, KB)
+        while (K // 128) % skg:
+            skg -= 1
+        parts = len(widths)
+        layer.append(dict(
+            name=gname, K=K, N=N, KB=KB, skg=skg, n0=[int(v) for v in np.cumsum([0] + widths[:-1])],
+            x=torch.from_numpy(WL.activations_f16(M, K, 30 + gi)).to(dev),
+            suh=[torch.from_numpy(WL.signs(K, 10 + 3 * gi + j)).to(dev) for j in range(parts)],
+            a=[torch.empty((M, K), dtype=torch.float16, device=dev) for _ in range(parts)],
+            words=[torch.randint(-2**31, 2**31 - 1, (nw,), dtype=torch.int32, device=dev, generator=gen)
+                   for _ in range(copies)],
+            svh=torch.from_numpy(WL.svh_scales(N, 20 + gi)).to(dev),
+            ws=torch.empty(max(1, skg * M * N), dtype=torch.float32, device=dev),
+            tickets=api.TicketBuffer(N, dev).t, out=torch.empty((M, N), dtype=torch.bfloat16, device=dev)))
+    return layer, copies, wbytes
+
+
+def config1_steps(api, layer, copies, out_scale):
+    """(two-launch step, fused step) closures over weight copy c: the input transforms (nout = parts) then one
+    r4dx_gemm_trellis_nt_m64_parts per group; or one r4dx_trellis_gemv_xf_parts per group (the transform inside)."""
+    def two(c):
+        for L in layer:
+            api.trellis_input(L["x"], L["suh"], 0, bf16=False, outs=L["a"])
+        for L in layer:
+            api.trellis_gemm_m64_parts(L["a"], L["n0"], L["words"][c], L["svh"], L["K"], L["N"], L["KB"],
+                                       skg=L["skg"], out=L["out"], ws=L["ws"], tickets=L["tickets"],
+                                       out_scale=out_scale)
+
+    def fused(c):
+        for L in layer:
+            api.trellis_gemv_xf_parts(L["x"], L["suh"], L["n0"], L["words"][c], L["svh"], L["K"], L["N"], L["KB"],
+                                      skg=L["skg"], out=L["out"], ws=L["ws"], tickets=L["tickets"],
+                                      out_scale=out_scale)
+    return two, fused
+
+
+def bench_config1_rows(api, WL, reps=4):
+    """Config 1's other step rows: the layer at M = 2, 4, 8 (KB 4), at KB 5 (M = 1, 8) and at the 4/5 mix (M = 1, 8),
+    each as the two-launch step (6 transforms + 6 parts launches) and as the fused step (6 r4dx_trellis_gemv_xf_parts
+    launches), replayed from HIP graphs over > 1 GiB of rotating weight copies. GB/s = weight bytes per step / step
+    time."""
+    import numpy as np
+    import torch
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(99)
+    out_scale = float(np.float32(1.0 / np.sqrt(128.0)))
+    rows = {}
+    cases = [("KB4", 2), ("KB4", 4), ("KB4", 8), ("KB5", 1), ("KB5", 8), ("mix", 1), ("mix", 8)]
+    for rate, M in cases:
+        kb_of = (lambda g: 4) if rate == "KB4" else (lambda g: 5) if rate == "KB5" else (lambda g: 5 if g in MIX_KB5 else 4)
+        layer, copies, wbytes = config1_layer(api, WL, M, kb_of, gen)
+        two, fused = config1_steps(api, layer, copies, out_scale)
+        rec = {"weight_bytes_per_step": wbytes, "copies": copies}
+        for form, fn in (("two_launch", two), ("fused", fused)):
+            ms = _graph_ms(lambda: [fn(c) for c in range(copies)], reps, copies)
+            rec[form + "_us"] = round(ms * 1e3, 2)
+            rec[form + "_GBs"] = round(wbytes / (ms * 1e-3) / 1e9, 1)
+        rows[f"{rate}_M{M}"] = rec
+        del layer
+        torch.cuda.empty_cache()
+    return {"workload": "config 1 layer, 6 launch groups; two_launch = transforms + parts GEMVs, fused = "
+                        "r4dx_trellis_gemv_xf_parts; mix = GDN and attention at KB 5, MLP at KB 4", "rows": rows}
 
 
 def pmc_prefill(api, WL, KB):

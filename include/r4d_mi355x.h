@@ -62,6 +62,15 @@ void r4dx_trellis_gemv_xf(int64_t x, int x_is_bf16, int64_t suh0, int64_t suh1, 
                           int64_t w, int64_t svh, int64_t c, int64_t ws, int64_t tickets, int M, int K, int N, int KB,
                           int SKG, float out_scale, int64_t stream);
 const char* r4dx_trellis_gemv_xf_check(int M, int K, int N, int n_split, int KB, int SKG, int have_ws);
+/* No reference counterpart (the engine runs r4dx_trellis_input_bf16 with nout suh, then one GEMV per projection): the
+ * input transform fused into r4dx_gemm_trellis_nt_m64_parts -- projections that read one input x (q | k | v, gdn
+ * qkv | z), stored as one linear, as ONE launch; columns [n0[p], n0[p + 1]) use suh[p] (host arrays of `parts`, 1..4,
+ * n0 as for _parts). Bit-identical to the transform followed by the parts launch at the same SKG. */
+const char* r4dx_trellis_gemv_xf_parts_check(int parts, const int* n0, int M, int K, int N, int KB, int SKG,
+                                             int have_ws);
+void r4dx_trellis_gemv_xf_parts(int64_t x, int x_is_bf16, const int64_t* suh, const int* n0, int parts,
+                                int prescale_log2, int64_t w, int64_t svh, int64_t c, int64_t ws, int64_t tickets,
+                                int M, int K, int N, int KB, int SKG, float out_scale, int64_t stream);
 
 /* No reference counterpart: for callers that cannot allocate or hold a workspace (code under HIP graph capture,
  * serving loops that forbid hipMalloc). r4d_gemm_trellis_nt_m64 (same C, A parts, SK and SKG meaning) with no ws or

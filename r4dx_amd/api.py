@@ -383,6 +383,37 @@ def trellis_gemv_xf(x, suh, w, svh, K, N, KB, skg=None, suh1=None, n_split=None,
     return out
 
 
+def trellis_gemv_xf_parts(x, suh_parts, n0, w, svh, K, N, KB, skg=None, prescale=0, bf16=False, out=None, ws=None,
+                          tickets=None, out_scale=1.0, stream=None):
+    """r4dx_trellis_gemv_xf_parts: the input transform fused into the parts launch -- columns [n0[p], n0[p + 1]) use
+    suh_parts[p]; x f16/bf16 bits [M][K] -> C bf16 [M][N]."""
+    L = lib()
+    M = x.shape[0]
+    parts = len(suh_parts)
+    if skg is None:   # the planner's split, lowered to whole 128-blocks per slice
+        skg = trellis_gemv_skg(K, N, KB)
+        while (K // 128) % skg:
+            skg -= 1
+    have_ws = skg > 1 or (ws is not None and tickets is not None)
+    n0a = (C.c_int * parts)(*n0)
+    msg = L.r4dx_trellis_gemv_xf_parts_check(parts, n0a, M, K, N, KB, skg, int(have_ws))
+    if msg:
+        raise ValueError(msg.decode())
+    if x.shape != (M, K) or svh is None or not -24 <= prescale <= 24:
+        raise ValueError("x is [M][K], svh is required, |prescale| <= 24")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    if have_ws and ws is None:
+        ws = torch.empty(max(1, skg * M * N), dtype=torch.float32, device=x.device)
+    if have_ws and tickets is None:
+        tickets = TicketBuffer(N, x.device).t
+    sa = (C.c_int64 * parts)(*[s.data_ptr() for s in suh_parts])
+    L.r4dx_trellis_gemv_xf_parts(_p(x), int(bf16), sa, n0a, parts, prescale, _p(w), _p(svh), _p(out),
+                                 _p(ws) if have_ws else 0, _p(tickets) if have_ws else 0, M, K, N, KB, skg,
+                                 float(out_scale), _stream(stream))
+    return out
+
+
 def trellis_input_i8(x, suh_list, prescale=0, row_scale=False, outs=None, stream=None):
     """The input transform fused with the activation quantizer (r4dx_trellis_input_i8 / _i8r): x bf16 bits
     [256][K] -> per output (a8 A8 layout, sa [K/128][256] or [256]); outs: preallocated (a8, sa) pairs."""

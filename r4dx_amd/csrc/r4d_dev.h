@@ -52,10 +52,18 @@ inline R4AParts r4_parts(const void* a0, const void* a1, int n_split, const void
   ap.n_end[2] = a3 ? n_end2 : 0x7FFFFFFF;
   return ap;
 }
-// the input of the 128-column group starting at column n0 (uniform per workgroup: scalar compares)
+// the part (0..3) of the 128-column group starting at column n0, and its input (uniform per workgroup: scalar
+// compares)
+__device__ __forceinline__ int r4_part_idx(const R4AParts& ap, int n0) {
+  return n0 < ap.n_end[0] ? 0 : n0 < ap.n_end[1] ? 1 : n0 < ap.n_end[2] ? 2 : 3;
+}
 __device__ __forceinline__ const unsigned short* r4_part_a(const R4AParts& ap, int n0) {
   return n0 < ap.n_end[0] ? ap.a[0] : n0 < ap.n_end[1] ? ap.a[1] : n0 < ap.n_end[2] ? ap.a[2] : ap.a[3];
 }
+// The input-transform sign vectors (suh) of a fused-transform launch's parts, selected like R4AParts' inputs.
+struct R4SParts {
+  const float* s[4];
+};
 
 typedef _Float16 r4h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 r4h2 __attribute__((ext_vector_type(2)));

@@ -64,8 +64,9 @@ struct r4d_gemv_args {
   int M, K, N, KB, SKG, full;
   float out_scale;
   int64_t stream;
-  // the fused input transform (r4dx_trellis_gemv_xf): xf = 1 for f16 x, 2 for bf16 x in a0; suh per part
-  int64_t suh0, suh1;
+  // the fused input transform (r4dx_trellis_gemv_xf / _xf_parts): xf = 1 for f16 x, 2 for bf16 x in a0; suh per
+  // part (the parts' column starts as for the A parts below: n_split, n_end1, n_end2)
+  int64_t suh0, suh1, suh2, suh3;
   int xf;
   float xscale;
   // SK = 1: one wave per tile pair over the whole K slice (the workgroup holds a 128-column group) also

@@ -90,14 +90,14 @@ constexpr int kRedParts = 8;         // the final slice sum is 8 interleaved run
 constexpr int kRedRows = 4;          // rows of the final slice sum per pass (8 measured slower at M = 8: LDS)
 
 // XF > 0: A0 is the raw input x [M][K] (XF 1: f16, 2: bf16) and the workgroup stages its own slice of the
-// transformed A = f16(FWHT128(fp32(x) * suh) * xscale) (suh0 / suh1 by column part) straight into LDS --
+// transformed A = f16(FWHT128(fp32(x) * suh) * xscale) (suh of the group's column part) straight into LDS --
 // the arithmetic of r4dx_trellis_input_*, so A is bit-identical to the unfused path's.
 template <int KB, int MT, int NPW, int SK, bool ALDS, int XF, bool WQ = false>
 __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     const R4AParts ap,
     const unsigned* __restrict__ W, const float* __restrict__ svh, void* __restrict__ Cv,
     float* __restrict__ ws, unsigned* __restrict__ tickets, int M, int K, int N, int SKG, int full,
-    float out_scale, const float* __restrict__ suh0, const float* __restrict__ suh1, float xscale,
+    float out_scale, const R4SParts sp, float xscale,
     unsigned long long* __restrict__ clk, const float* __restrict__ wsc, int wq_gsh) {
   // steps in flight; 2 where each ring slot also carries MT row tiles of A from global memory (4 slots of 4 row
   // tiles would not fit the VGPRs and spill)
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
   // weights waits for them.
   constexpr int kXfPre = 6;
   const int xf_nblk = (ktl_pad + 7) >> 3;
-  const float* __restrict__ suh_p = group * 128 >= n_split ? suh1 : suh0;
+  const float* __restrict__ suh_p = sp.s[r4_part_idx(ap, group * 128)];
   struct XfIn {
     unsigned x2;   // x[2l], x[2l + 1] (f16 or bf16 bits)
     r4f2 s2;       // suh[2l], suh[2l + 1]
@@ -602,10 +602,15 @@ void launch_gemv(const r4d_gemv_args& a) {
   }
   const R4AParts ap = r4_parts((const void*)a.a0, (const void*)a.a1, a.n_split, (const void*)a.a2, a.n_end1,
                                (const void*)a.a3, a.n_end2);
+  R4SParts sp;
+  sp.s[0] = (const float*)a.suh0;
+  sp.s[1] = (const float*)(a.suh1 ? a.suh1 : a.suh0);
+  sp.s[2] = a.suh2 ? (const float*)a.suh2 : sp.s[1];
+  sp.s[3] = a.suh3 ? (const float*)a.suh3 : sp.s[2];
   hipLaunchKernelGGL((tq_gemv_kernel<KB, MT, NPW, SK, ALDS, XF, WQ>), grid, block, smem, (hipStream_t)a.stream, ap,
                      (const unsigned*)a.w, (const float*)a.svh, (void*)a.c, (float*)a.ws,
-                     (unsigned*)a.tickets, a.M, a.K, a.N, a.SKG, a.full, a.out_scale, (const float*)a.suh0,
-                     (const float*)(a.suh1 ? a.suh1 : a.suh0), a.xscale, (unsigned long long*)a.clk,
+                     (unsigned*)a.tickets, a.M, a.K, a.N, a.SKG, a.full, a.out_scale, sp, a.xscale,
+                     (unsigned long long*)a.clk,
                      (const float*)a.wsc, a.wq_gsh);
 }
 
@@ -807,6 +812,44 @@ void r4dx_trellis_gemv_xf(int64_t x, int x_is_bf16, int64_t suh0, int64_t suh1, 
   a.suh1 = suh1;
   a.xf = x_is_bf16 ? 2 : 1;
   // float(2^s / sqrt(128)), rounded once from double (trellis_ref.hpp:146-148)
+  a.xscale = (float)(__builtin_ldexp(1.0, prescale_log2) / __builtin_sqrt(128.0));
+  if (a.KB == 4) launch_gemv_kb<4>(a);
+  else if (a.KB == 5) launch_gemv_kb<5>(a);
+  else launch_gemv_kb<3>(a);
+  r4d::launch_ok(entry);
+}
+
+// No reference counterpart: r4dx_trellis_gemv_xf over up to four column parts, each with its own suh -- the input
+// transform of r4dx_trellis_input_* (nout = parts) fused into r4dx_gemm_trellis_nt_m64_parts: projections that read
+// one input x (q | k | v, gdn qkv | z) stored as one linear run as ONE launch. Columns [n0[p], n0[p + 1]) use suh[p];
+// every column equals the two-launch form (the transform, then the parts launch at the same SKG) bit for bit.
+const char* r4dx_trellis_gemv_xf_parts_check(int parts, const int* n0, int M, int K, int N, int KB, int SKG,
+                                             int have_ws) {
+  const std::string e = r4d::parts_rule(parts, n0, N);
+  if (!e.empty()) return r4d::check_result(e);
+  return r4dx_trellis_gemv_xf_check(M, K, N, parts > 1 ? n0[1] : N, KB, SKG, have_ws);
+}
+
+void r4dx_trellis_gemv_xf_parts(int64_t x, int x_is_bf16, const int64_t* suh, const int* n0, int parts,
+                                int prescale_log2, int64_t w, int64_t svh, int64_t c, int64_t ws, int64_t tickets,
+                                int M, int K, int N, int KB, int SKG, float out_scale, int64_t stream) {
+  const char* entry = "trellis_gemv_xf_parts";
+  if (!suh || !n0) r4d::fail(entry, "null part arrays");
+  if (!x || !w || !c || !svh) r4d::fail(entry, "null x, W, svh or C");
+  if (prescale_log2 < -24 || prescale_log2 > 24) r4d::fail(entry, "|prescale_log2| must be <= 24");
+  if (const char* m = r4dx_trellis_gemv_xf_parts_check(parts, n0, M, K, N, KB, SKG, ws != 0 && tickets != 0))
+    r4d::fail(entry, m);
+  for (int p = 0; p < parts; ++p)
+    if (!suh[p]) r4d::fail(entry, "null part suh");
+  r4d_gemv_args a{x, parts > 1 ? x : 0, parts > 1 ? n0[1] : N, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale,
+                  stream};
+  if (parts > 2) { a.a2 = x; a.n_end1 = n0[2]; }
+  if (parts > 3) { a.a3 = x; a.n_end2 = n0[3]; }
+  a.suh0 = suh[0];
+  a.suh1 = parts > 1 ? suh[1] : 0;
+  a.suh2 = parts > 2 ? suh[2] : 0;
+  a.suh3 = parts > 3 ? suh[3] : 0;
+  a.xf = x_is_bf16 ? 2 : 1;
   a.xscale = (float)(__builtin_ldexp(1.0, prescale_log2) / __builtin_sqrt(128.0));
   if (a.KB == 4) launch_gemv_kb<4>(a);
   else if (a.KB == 5) launch_gemv_kb<5>(a);

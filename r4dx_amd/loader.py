@@ -61,6 +61,8 @@ SIGS = {
     "r4d_gemm_trellis_nt_i8c": (None, [I64, I64, I64, I64, I32] + [I64] * 6 + [I32] * 6 + [F32, I64]),
     "r4dx_trellis_gemv_xf": (None, [I64, I32, I64, I64, I32, I32] + [I64] * 5 + [I32] * 5 + [F32, I64]),
     "r4dx_trellis_gemv_xf_check": (CSTR, [I32] * 7),
+    "r4dx_trellis_gemv_xf_parts_check": (CSTR, [I32, I32P] + [I32] * 6),
+    "r4dx_trellis_gemv_xf_parts": (None, [I64, I32, I64P, I32P, I32, I32] + [I64] * 5 + [I32] * 5 + [F32, I64]),
     "r4dx_trellis_input_i8": (None, [I64, I64, I64, I32, I64P, I64P, I64P, I32, I64]),
     "r4dx_trellis_input_i8r": (None, [I64, I64, I64, I32, I64P, I64P, I64P, I32, I64]),
     "r4dx_trellis_input_bf16": (None, [I64, I64, I64, I32, I64P, I64P, I32, I64]),

@@ -232,3 +232,31 @@ def test_parts_launch_equals_one_launch_per_projection(M, KB, widths):
         assert np.array_equal(whole[:, c0:c0 + wdt], one), p
         ref = O.linear_from_a(a[p], np.ascontiguousarray(q[:, c0:c0 + wdt]), svh[c0:c0 + wdt])
         assert close_rel(O.bf16_bits_to_f32(whole[:, c0:c0 + wdt]), ref, 2.0**-8, 1e-3) <= 1.0
+
+
+@pytest.mark.parametrize("M,KB,widths,bf16,prescale", [(1, 4, (6144, 1024, 1024), False, 0),
+                                                        (1, 4, (10240, 6144), True, 0), (8, 5, (10240, 6144), False, 2),
+                                                        (4, 4, (256, 128, 384, 256), True, -3),
+                                                        (2, 3, (1024, 512, 512), False, 0)])
+def test_xf_parts_equals_transform_then_parts(M, KB, widths, bf16, prescale):
+    """r4dx_trellis_gemv_xf_parts (the transform fused into the parts launch) == r4dx_trellis_input_* with one output
+    per part, then r4dx_gemm_trellis_nt_m64_parts at the same SKG, byte for byte."""
+    banner("xf parts", M, KB, widths, bf16, prescale)
+    K = 5120 if widths[0] > 1024 else 1024
+    N = sum(widths)
+    n0 = [int(v) for v in np.concatenate([[0], np.cumsum(widths)[:-1]])]
+    rng = np.random.default_rng(N + M)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to("cuda")
+    xb = (x.to(torch.bfloat16) if bf16 else x.half()).view(torch.int16)
+    suh = [dev(WL.signs(K, 20 + p)) for p in range(len(widths))]
+    words, svh = dev(WL.trellis_words(K, N, KB, 12)), dev(WL.svh_scales(N, 13))
+    skg = api.trellis_gemv_skg(K, N, KB)
+    while (K // 128) % skg:
+        skg -= 1
+    osc = float(np.float32(1.0 / np.sqrt(128.0)))
+    a = [o for i in range(0, len(suh), 3) for o in api.trellis_input(xb, suh[i:i + 3], prescale, bf16=bf16)]
+    ref = api.trellis_gemm_m64_parts(a, n0, words, svh, K, N, KB, skg=skg, out_scale=osc)
+    got = api.trellis_gemv_xf_parts(xb, suh, n0, words, svh, K, N, KB, skg=skg, prescale=prescale, bf16=bf16,
+                                    out_scale=osc)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
