@@ -458,7 +458,7 @@ def bench_m256(api, WL, KB, R=3):
         a = torch.from_numpy(WL.activations_f16(M, K, 40 + i, outlier_frac=0.01)).to(dev)
         svh = torch.from_numpy(WL.svh_scales(N, 50 + i)).to(dev)
         skg = api.trellis_m256_skg(K, N, KB)
-        ws = torch.empty(max(1, skg * M * N), dtype=torch.float32, device=dev)
+        ws = torch.empty(api.lib().r4d_gemm_trellis_nt_m256_ws_bytes(M, N, skg) // 4, dtype=torch.float32, device=dev)
         tk = api.TicketBuffer(N, dev).t
         out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
 
@@ -509,7 +509,7 @@ def bench_m256(api, WL, KB, R=3):
              for j in range(len(names))]
         svh = torch.from_numpy(WL.svh_scales(N, 70 + i)).to(dev)
         skg = api.trellis_m256_skg(K, N, KB)
-        ws = torch.empty(max(1, skg * M * N), dtype=torch.float32, device=dev)
+        ws = torch.empty(api.lib().r4d_gemm_trellis_nt_m256_ws_bytes(M, N, skg) // 4, dtype=torch.float32, device=dev)
         tk = api.TicketBuffer(N, dev).t
         out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
 
@@ -710,7 +710,7 @@ def bench_trellis_i8(api, WL, KB, R=4):
         svh = torch.from_numpy(WL.svh_scales(N, 8)).to(dev)
         out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
         skg = 1 if N > 8192 else 4
-        ws = torch.empty(max(1, skg * M * N), dtype=torch.float32, device=dev)
+        ws = torch.empty(api.lib().r4d_gemm_trellis_nt_m256_ws_bytes(M, N, skg) // 4, dtype=torch.float32, device=dev)
         xb = torch.from_numpy(WL.activations_f16(M, K, 7, outlier_frac=0.01).astype("float32")).to(dev) \
             .to(torch.bfloat16).view(torch.int16)
         suh = torch.from_numpy(WL.signs(K, 9)).to(dev)

@@ -125,8 +125,10 @@ def trellis_gemm_m256_parts(a_parts, n0, w, svh, K, N, KB, skg=None, out=None, w
         raise ValueError(msg.decode())
     if any(a.shape != (M, K) for a in a_parts) or svh is None:
         raise ValueError("every part input is [M][K]; svh is required")
-    if ws is None and skg > 1:
+    if ws is None:
         ws = torch.empty(L.r4d_gemm_trellis_nt_m256_ws_bytes(M, N, skg) // 4, dtype=torch.float32, device=w.device)
+    if tickets is None:
+        tickets = TicketBuffer(N, w.device).t
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=w.device)
     pa = (C.c_int64 * parts)(*[a.data_ptr() for a in a_parts])
@@ -154,10 +156,12 @@ def trellis_gemm_m256(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out
         if raw:
             raise ValueError("r4d_gemm_trellis_nt_m256_wq has no raw form")
         _wq_args(wq, K, KB)
-    if ws is None and skg > 1:
+    # ws and tickets as the reference requires them (r4d.h:406-407): the split slices and the balanced form's
+    # hand-over of cut units use them
+    if ws is None:
         ws = torch.empty(L.r4d_gemm_trellis_nt_m256_ws_bytes(M, N, skg) // 4, dtype=torch.float32,
                          device=a0.device)
-    if tickets is None and skg > 1:
+    if tickets is None:
         tickets = TicketBuffer(N, a0.device).t
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32 if raw else torch.bfloat16, device=a0.device)

@@ -41,6 +41,10 @@ MIN_OCCUPANCY = [            # (demangled name prefix, waves per SIMD at least):
     ("w4_kernel<", 4),
     ("am_kernel<", 8),
 ]
+# Kernels allowed a few SGPR spills (at most this many; they go to VGPR lanes by v_writelane, never to memory, and the
+# gate still requires no scratch and no VGPR spill): the prefill GEMM keeps its launch arguments and the per-segment
+# geometry of the balanced form in scalars across the whole kernel, outside the step loop.
+SGPR_LANE_SPILLS = [("tq_m256_kernel<", 16)]
 
 
 def parse_resources(text):
@@ -73,7 +77,8 @@ def gate(recs):
     bad = []
     for r in recs:
         name = r.get("name", r["mangled"])
-        if r.get("ScratchSize", 0) or r.get("VGPRsSpill", 0) or r.get("SGPRsSpill", 0):
+        sgpr_ok = max([n for prefix, n in SGPR_LANE_SPILLS if name.startswith(prefix)] or [0])
+        if r.get("ScratchSize", 0) or r.get("VGPRsSpill", 0) or r.get("SGPRsSpill", 0) > sgpr_ok:
             bad.append(f"{name}: scratch {r.get('ScratchSize')} B/lane, VGPR spill {r.get('VGPRsSpill')}, "
                        f"SGPR spill {r.get('SGPRsSpill')}")
         for prefix, occ in MIN_OCCUPANCY:

@@ -83,6 +83,13 @@ __device__ __forceinline__ unsigned short r4_bf16_rn(float f) {
   if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (unsigned short)((u >> 16) | 0x40u);
   return (unsigned short)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
+// The same rounding as a select (no branch): in a fully unrolled epilogue an early return becomes divergent control
+// flow per element.
+__device__ __forceinline__ unsigned short r4_bf16_rn_sel(float f) {
+  const unsigned u = __builtin_bit_cast(unsigned, f);
+  const unsigned rn = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16, qnan = (u >> 16) | 0x40u;
+  return (unsigned short)((u & 0x7FFFFFFFu) > 0x7F800000u ? qnan : rn);
+}
 // fp32 -> f16 bits, nearest even (v_cvt_f16_f32 under the default round mode). The empty asm keeps
 // the caller's fp32 value an fp32 value: without it a preceding multiply may be folded into a
 // v_fma_mix with a single rounding, which is not the reference's two-rounding arithmetic.

@@ -93,7 +93,11 @@ def test_m256_checks(L):
     assert ck(256, 5120, 5120, 5120, 4, 2, 1, 2, 4, 2) is None and ck(256, 5120, 5120, 5120, 4, 1, 1, 2, 4, 0) is None
     for sk in (4, 8, 16):
         assert b"SK must be 1 or 2" in ck(256, 5120, 5120, 5120, 4, sk, 1, 2, 4, 4)
-    assert L.r4d_gemm_trellis_nt_m256_ws_bytes(256, 5120, 2) == 2 * 256 * 5120 * 4
+    # SKG slices, then (SKG > 1) the balanced form's hand-over area: M x 128 fp32 for each of min(units, CUs)
+    # workgroups (no GPU here: 256 CUs assumed); SKG = 1 needs no more than the M x N floats
+    assert L.r4d_gemm_trellis_nt_m256_ws_bytes(256, 5120, 2) == 2 * 256 * 5120 * 4 + 80 * 256 * 128 * 4
+    assert L.r4d_gemm_trellis_nt_m256_ws_bytes(256, 5120, 8) == 8 * 256 * 5120 * 4 + 256 * 256 * 128 * 4
+    assert L.r4d_gemm_trellis_nt_m256_ws_bytes(256, 34816, 1) == 256 * 34816 * 4
     for K, N in [(5120, 17408), (17408, 5120), (5120, 1024), (6144, 5120)]:
         skg = L.r4d_mi355x_trellis_m256_skg(K, N, 4)
         assert ck(256, K, N, N, 4, 0, 0, skg, 0, 0) is None

@@ -49,6 +49,8 @@ def test_m256_raw_full(KB, K, N, M, skg):
 @pytest.mark.parametrize("M,K,N,KB,skg", [
     (256, 1024, 384, 4, 1), (256, 2048, 256, 5, 2), (128, 1024, 256, 4, 4), (256, 5120, 256, 4, 10),
     (256, 5120, 384, 3, 16), (128, 2560, 128, 5, 5), (256, 17408, 128, 4, 34),
+    # the balanced form (more units than compute units, not a multiple of them): cut units handed on
+    (256, 5120, 34816, 4, 1), (256, 17408, 5120, 4, 8), (128, 1024, 33024, 5, 1), (256, 2048, 8320, 4, 4),
 ])
 def test_m256_bit_identical_to_m64_rows(M, K, N, KB, skg):
     """r4d.h:402-412: every element of the M = 256 (128) launch equals, bit for bit, what the M <= 64 kernel
@@ -150,3 +152,23 @@ def test_m256_parts_equals_one_launch_per_projection(M, KB, widths):
         if check_oracle and p > 0:
             ref = O.linear_from_a(a[p], np.ascontiguousarray(q[:, c0:c0 + wdt]), svh[c0:c0 + wdt])
             assert close_rel(O.bf16_bits_to_f32(whole[:, c0:c0 + wdt]), ref, 2.0**-8, 1e-3) <= 1.0
+
+
+def test_m256_balanced_repeats_and_resets_flags():
+    """The balanced form (272 units on 256 CUs): repeated launches on one ws and ticket buffer give the same bits,
+    and every hand-over flag is back at zero after each launch (the reader resets it)."""
+    banner("m256 balanced repeats")
+    M, K, N, KB = 256, 2048, 34816, 4
+    words, _, svh = WL.trellis_linear(K, N, KB, 99)
+    a = WL.activations_f16(M, K, 5, outlier_frac=0.01).view(np.uint16)
+    w_d, a_d, s_d = dev(words), dev(a), dev(svh)
+    ws = torch.empty(api.lib().r4d_gemm_trellis_nt_m256_ws_bytes(M, N, 1) // 4, dtype=torch.float32, device="cuda")
+    tk = api.TicketBuffer(N).t
+    first = api.trellis_gemm_m256(a_d, w_d, s_d, K, N, KB, skg=1, ws=ws, tickets=tk, out_scale=0.25)
+    torch.cuda.synchronize()
+    assert int(tk.abs().sum().item()) == 0
+    for _ in range(5):
+        again = api.trellis_gemm_m256(a_d, w_d, s_d, K, N, KB, skg=1, ws=ws, tickets=tk, out_scale=0.25)
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int16), first.view(torch.int16))
+        assert int(tk.abs().sum().item()) == 0
