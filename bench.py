@@ -270,6 +270,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(KB)
+        cpu["other_legs"] = cpu_baselines_other(KB)
 
     value = layer_wbytes / (ms_step * 1e-3) / 1e9
     line = {
@@ -557,7 +558,7 @@ def bench_m256(api, WL, KB, R=3):
             "per_projection_TFLOPs": round(per_proj, 1), "per_shape": per_shape}
 
 
-def bench_w4a16(api, WL, R=4):
+def bench_w4a16(api, WL, R=8):
     """the w4a16 LM head (N = 248 320, K = 5120) at groups 32 / 64 and M = 1 / 8, fp32
     logits + per-row argmax. GB/s = (N K / 2 + N K / g * 4) bytes over the GEMM's average launch time
     (back-to-back in a HIP graph over 2 weight copies, > the 256 MB MALL)."""
@@ -581,31 +582,45 @@ def bench_w4a16(api, WL, R=4):
                     api.w4a16_gemm(a, wq_d, wsz_d, K, N, g, out=out, f32=True)
                     if with_argmax:
                         api.argmax_rows(out, idx, val)
-            times = {}
-            for with_am in (False, True):
+            # the argmax alone (one launch over the logits the GEMM left), the GEMM, and the GEMM with the argmax: three
+            # graphs, each replayed in three interleaved rounds (the median per graph), so that clock drift between
+            # measurements does not land on one of them
+            def run_am():
+                for _ in copies:
+                    api.argmax_rows(out, idx, val)
+            graphs = {}
+            for with_am in (None, False, True):
                 gr = torch.cuda.CUDAGraph()
                 s = torch.cuda.Stream()
                 s.wait_stream(torch.cuda.current_stream())
+                fn = run_am if with_am is None else (lambda wa=with_am: run(wa))
                 with torch.cuda.stream(s):
-                    run(with_am)   # eager once on the capture stream: the argmax allocates its scratch there
+                    fn()   # eager once on the capture stream: the argmax allocates its scratch there
                     torch.cuda.synchronize()
                     with torch.cuda.graph(gr, stream=s):
                         for _ in range(R):
-                            run(with_am)
+                            fn()
                 torch.cuda.synchronize()
                 gr.replay()
-                st = torch.cuda.current_stream()
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(st)
-                gr.replay()
-                e1.record(st)
                 torch.cuda.synchronize()
-                times[with_am] = e0.elapsed_time(e1) / (R * len(copies))
+                graphs[with_am] = gr
+            samples = {k: [] for k in graphs}
+            st = torch.cuda.current_stream()
+            for _ in range(3):
+                for k, gr in graphs.items():
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(st)
+                    gr.replay()
+                    e1.record(st)
+                    torch.cuda.synchronize()
+                    samples[k].append(e0.elapsed_time(e1) / (R * len(copies)))
+            times = {k: sorted(v)[1] for k, v in samples.items()}
             nbytes = N * K / 2 + N * K / g * 4
             res[f"g{g}_M{M}"] = {"gemm_us": round(times[False] * 1e3, 2),
                                  "GBs": round(nbytes / (times[False] * 1e-3) / 1e9, 1),
                                  "frac": round(nbytes / (times[False] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                 "gemm_plus_argmax_us": round(times[True] * 1e3, 2)}
+                                 "gemm_plus_argmax_us": round(times[True] * 1e3, 2),
+                                 "argmax_alone_us": round(times[None] * 1e3, 2)}
         del copies
         torch.cuda.empty_cache()
     return {"metric": "w4a16 LM head (N=248320, K=5120) effective HBM GB/s", "kernel": "w4_kernel",
@@ -785,6 +800,87 @@ def cpu_baseline(KB):
             "sample": f"config0 K=N=5120 KB={KB} M=1 (bf16 x): the reference's trellis_ref.hpp transform + "
                       f"pair-grid decode + fp64 linear, single-threaded as written, {reps} runs, {dt * 1e3:.1f} ms "
                       f"each", "port_all_cores": port}
+
+
+def cpu_baselines_other(KB):
+    """CPU rows beside the other legs, each on a bounded sample of its workload, median of 5 runs: decode alone and
+    decode + matmul for the trellis linear (config 0) and the M = 256 GEMM (config 2, a 1024-column sample), the int8
+    GEMM (config 4, a 256-column sample) and the w4a16 LM head (config 3, an 8192-row sample at g = 64, dequant alone
+    and dequant + matmul). The oracle's C restatement on all host cores ("port"); where oracle/_ref is built, the
+    reference's own single-threaded code ("reference": trellis_ref.hpp decode, int8_gemm_proto_ref.h RefGemmInt8)."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    from oracle_lib import ptr
+    from r4dx_amd import workloads as WL
+    lib, ref = O.lib(), O.ref()
+    cores = lib.r4o_max_threads()
+
+    def med(fn, n=5):
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    rows = {"cores_port": cores, "cores_reference": 1}
+    # config 0 / 2: decode alone, and decode + matmul at M = 1 (config 0) and M = 256 (a 1024-column sample)
+    K = N = 5120
+    words, suh, svh = WL.trellis_linear(K, N, KB, 1)
+    wbytes = K * N * KB / 8
+    t = med(lambda: O.decode_pair_grid(words, K, N, KB, 0))
+    rows["trellis_decode_only"] = {"value": round(wbytes / t / 1e9, 4), "unit": "GB/s", "kind": "port", "cores": cores,
+                                   "sample": f"config0 K=N=5120 KB={KB}: pair-grid decode to f16, {t * 1e3:.1f} ms"}
+    if ref is not None:
+        q = np.empty((K, N), np.uint16)
+        t = med(lambda: ref.ref_decode_pair_grid(ptr(words), K, N, KB, ptr(q)), 3)
+        rows["trellis_decode_only_reference"] = {
+            "value": round(wbytes / t / 1e9, 4), "unit": "GB/s", "kind": "reference", "cores": 1,
+            "sample": f"config0 K=N=5120 KB={KB}: trellis_ref.hpp DecodePairGrid, {t * 1e3:.1f} ms"}
+    Ns = 1024
+    w_s, _, _ = WL.trellis_linear(K, Ns, KB, 3)
+    a = WL.activations_f16(256, K, 4, outlier_frac=0.01).view(np.uint16)
+    t_dec = med(lambda: O.decode_pair_grid(w_s, K, Ns, KB, 0))
+    qs = O.decode_pair_grid(w_s, K, Ns, KB, 0)
+    t_mm = med(lambda: O.raw_sums(a, qs, nthreads=0), 3)
+    flop = 2.0 * 256 * K * Ns
+    rows["m256_decode_plus_matmul"] = {
+        "value": round(flop / (t_dec + t_mm) / 1e12, 5), "unit": "TFLOP/s", "kind": "port", "cores": cores,
+        "sample": f"config2 M=256 K=5120, {Ns} of the columns, KB={KB}: decode {t_dec * 1e3:.1f} ms + fp64 matmul "
+                  f"{t_mm * 1e3:.1f} ms"}
+    # config 4: the int8 GEMM, row scales, a 256-column sample
+    Ni = 256
+    x, w8, sw = WL.int8_case(K, Ni, 3)
+    sa = np.empty(256, np.float32)
+    a8 = np.empty((256, K), np.int8)
+    lib.r4o_i8_quant_act_row(ptr(np.ascontiguousarray(x.view(np.uint16))), 256, K, ptr(sa), ptr(a8))
+    c = np.empty((256, Ni), np.float64)
+    ops = 2.0 * 256 * K * Ni
+    t = med(lambda: lib.r4o_i8_gemm_ref(ptr(a8), ptr(sa), ptr(w8), ptr(sw), 256, Ni, K, 3, ptr(c), 0))
+    rows["int8_gemm"] = {"value": round(ops / t / 1e12, 5), "unit": "TOP/s", "kind": "port", "cores": cores,
+                         "sample": f"config4 M=256 K=5120, {Ni} of the columns, row scales: {t * 1e3:.1f} ms"}
+    if ref is not None:
+        t = med(lambda: ref.ref_i8_gemm(ptr(a8), ptr(sa), ptr(w8), ptr(sw), 256, Ni, K, 3, ptr(c)), 3)
+        rows["int8_gemm_reference"] = {"value": round(ops / t / 1e12, 5), "unit": "TOP/s", "kind": "reference",
+                                       "cores": 1, "sample": f"the same sample through int8_gemm_proto_ref.h "
+                                                             f"RefGemmInt8: {t * 1e3:.1f} ms"}
+    # config 3: the w4a16 LM head at g = 64, M = 1, an 8192-row sample: dequant alone, dequant + fp64 matmul
+    Nw, g = 8192, 64
+    wq, wsz = WL.w4a16_packed(Nw, K, g, 100)
+    xa = WL.activations_f16(1, K, 5).view(np.uint16)
+    wf = np.empty((Nw, K), np.float32)
+    y = np.empty((1, Nw), np.float64)
+    wb = Nw * K / 2 + Nw * K / g * 4
+    t = med(lambda: lib.r4o_w4_dequant(ptr(wq), ptr(wsz), Nw, K, g, ptr(wf)))
+    rows["w4a16_dequant_only"] = {"value": round(wb / t / 1e9, 4), "unit": "GB/s", "kind": "port", "cores": 1,
+                                  "sample": f"config3 K=5120 g=64, {Nw} of the vocab rows: dequant to fp32, "
+                                            f"{t * 1e3:.1f} ms"}
+    t = med(lambda: lib.r4o_w4_gemm_ref(ptr(xa), ptr(wq), ptr(wsz), 1, Nw, K, g, ptr(y), 0))
+    rows["w4a16_dequant_plus_matmul"] = {"value": round(wb / t / 1e9, 4), "unit": "GB/s", "kind": "port",
+                                         "cores": cores, "sample": f"the same sample, M=1: dequant + fp64 matmul, "
+                                                                   f"{t * 1e3:.1f} ms"}
+    return rows
 
 
 if __name__ == "__main__":
