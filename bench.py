@@ -426,6 +426,15 @@ def pmc_prefill(api, WL, KB):
         for _ in range(2):
             api.trellis_gemm_m256(a, words, svh, K, N, KB, out_scale=0.08838834764831845)
         order.append(["tq_m256_kernel", name, K, N, 2 * 256 * K * N])
+    # the merged gate | up launch of the 6-launch layer: 272 groups on 256 CUs, the balanced form
+    K, N = 5120, 34816
+    words = torch.randint(-2**31, 2**31 - 1, (K * N * KB // 32,), dtype=torch.int32, device=dev)
+    a = torch.from_numpy(WL.activations_f16(256, K, 60, outlier_frac=0.01)).to(dev)
+    svh = torch.from_numpy(WL.svh_scales(N, 61)).to(dev)
+    for _ in range(2):
+        api.trellis_gemm_m256(a, words, svh, K, N, KB, out_scale=0.08838834764831845)
+    order.append(["tq_m256_kernel", "mlp.gate|mlp.up (balanced)", K, N, 2 * 256 * K * N])
+    del words
     for K, N in ((5120, 17408), (17408, 5120)):
         x, w8, sw = WL.int8_case(K, N, 3)
         w_d, sw_d = api.i8_pack_w(torch.from_numpy(w8).to(dev)), torch.from_numpy(sw).to(dev)
@@ -439,6 +448,12 @@ def pmc_prefill(api, WL, KB):
         for _ in range(2):
             api.trellis_gemm_i8(a8, sa, words, swc, svh, K, N, KB, coarse=True, skg=1 if N > 8192 else 4)
         order.append(["ti8_gemm_kernel<4, 0, 0, false>", f"trellis coarse {K}x{N}", K, N, 2 * 256 * K * N])
+        # the per-128 form: per (row, 128 k) activation scales, per (column, 128 k) weight scales
+        a8b, sab = api.i8_quant(torch.from_numpy(x.view(np.uint16)).to(dev), True)
+        swb = api.trellis_i8_table(words, K, N, KB, False)
+        for _ in range(2):
+            api.trellis_gemm_i8(a8b, sab, words, swb, svh, K, N, KB, coarse=False, skg=1 if N > 8192 else 4)
+        order.append(["ti8_gemm_kernel<4, 2, 0, false>", f"trellis per-128 {K}x{N}", K, N, 2 * 256 * K * N])
     torch.cuda.synchronize()
     print(json.dumps({"pmc_prefill": "done", "launches_each": 2, "order": order}), flush=True)
 
