@@ -38,6 +38,7 @@ def parse():
     ap.add_argument("--no-rows", action="store_true", help="skip the config-1 rows at M 2/4/8, KB 5 and the mix")
     ap.add_argument("--no-w4", action="store_true", help="skip the w4a16 LM-head leg")
     ap.add_argument("--no-i8", action="store_true", help="skip the int8 prefill GEMM legs")
+    ap.add_argument("--no-vendor", action="store_true", help="skip the vendor-library GEMMs timed for context")
     ap.add_argument("--pmc-prefill", action="store_true",
                     help="counter pass for the prefill kernels: each config-2 M = 256 shape, then the config-4 "
                          "dense and trellis int8 GEMMs, launched twice each; prints the launch order, no JSON line")
@@ -266,6 +267,7 @@ def main():
     w4 = None if args.no_w4 else bench_w4a16(api, WL)
     i8 = None if args.no_i8 else bench_int8(api, WL)
     ti8 = None if args.no_i8 else bench_trellis_i8(api, WL, KB)
+    vendor = None if args.no_vendor else bench_vendor(WL)
 
     cpu = None
     if not args.no_cpu:
@@ -315,6 +317,7 @@ def main():
         "w4a16": w4,
         "int8": i8,
         "trellis_int8": ti8,
+        "vendor_gemm": vendor,
         "wall_s": round(wall, 3),
     }
     print(json.dumps(line), flush=True)
@@ -640,6 +643,82 @@ def bench_w4a16(api, WL, R=8):
         torch.cuda.empty_cache()
     return {"metric": "w4a16 LM head (N=248320, K=5120) effective HBM GB/s", "kernel": "w4_kernel",
             "peak_GBs": HBM_PEAK_GBS, "cases": res}
+
+
+def bench_vendor(WL, R=4):
+    """Context for the prefill legs, not a product path: the vendor library's plain GEMMs (hipBLASLt through
+    torch.matmul, f16 weights, no decode; torch._int_mm, int8 weights) on the same launch shapes. f16: the config-2
+    layer's 6 launches (same-input projections concatenated along N) at M = 256; int8: the two config-4 shapes.
+    Best of the two weight layouts ([N][K] read transposed, [K][N]); rotating weight copies (> 1 GB per shape);
+    back-to-back launches in a HIP graph (eager if the capture fails)."""
+    import numpy as np
+    import torch
+    dev = torch.device("cuda:0")
+    M = 256
+
+    def timed(fn, n):
+        try:
+            fn()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(g, stream=s):
+                    for _ in range(R):
+                        fn()
+            torch.cuda.synchronize()
+            g.replay()
+            run = g.replay
+            reps = 1
+        except RuntimeError:
+            run, reps = fn, R
+        torch.cuda.synchronize()
+        st = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(reps):
+            run()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (R * n)
+
+    shape = {name: (K, N) for name, K, N in WL.LAYER_SHAPES}
+    f16, tot_flop, tot_ms = {}, 0.0, 0.0
+    for gname, members in WL.LAYER_GROUPS:
+        names = [p for m in members for p in m]
+        K, N = shape[names[0]][0], sum(shape[p][1] for p in names)
+        a = torch.randn((M, K), dtype=torch.float16, device=dev)
+        copies = max(2, int(np.ceil(1.0e9 / (K * N * 2))))
+        best = None
+        for layout in ("nk", "kn"):
+            w = [torch.randn((N, K) if layout == "nk" else (K, N), dtype=torch.float16, device=dev)
+                 for _ in range(copies)]
+            ms = timed(lambda: [a @ (x.t() if layout == "nk" else x) for x in w], copies)
+            best = ms if best is None else min(best, ms)
+            del w
+        torch.cuda.empty_cache()
+        flop = 2.0 * M * K * N
+        f16["|".join(names)] = {"us": round(best * 1e3, 2), "TFLOPs": round(flop / (best * 1e-3) / 1e12, 1)}
+        tot_flop += flop
+        tot_ms += best
+    i8 = {}
+    for K, N in ((5120, 17408), (17408, 5120)):
+        a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev)
+        copies = max(2, int(np.ceil(1.0e9 / (K * N))))
+        best = None
+        for layout in ("nk", "kn"):
+            w = [torch.randint(-127, 128, (N, K) if layout == "nk" else (K, N), dtype=torch.int8, device=dev)
+                 for _ in range(copies)]
+            ms = timed(lambda: [torch._int_mm(a, x.t() if layout == "nk" else x) for x in w], copies)
+            best = ms if best is None else min(best, ms)
+            del w
+        torch.cuda.empty_cache()
+        i8[f"K{K}_N{N}"] = {"us": round(best * 1e3, 2), "TOPs": round(2.0 * M * K * N / (best * 1e-3) / 1e12, 1)}
+    return {"what": "vendor library plain GEMMs on the same shapes (context, no decode): torch.matmul f16 "
+                    "(hipBLASLt) and torch._int_mm int8",
+            "f16_layer_us": round(tot_ms * 1e3, 1), "f16_layer_TFLOPs": round(tot_flop / (tot_ms * 1e-3) / 1e12, 1),
+            "f16_per_launch": f16, "int8": i8}
 
 
 def _traffic(kernel, KB, M, names):
