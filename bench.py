@@ -778,8 +778,8 @@ def bench_int8(api, WL, R=4):
         ws_ = [w_d] + [w_d.clone() for _ in range(copies - 1)]
         sw_d = torch.from_numpy(sw).to(dev)
         x_d = torch.from_numpy(x.view("int16")).to(dev)
-        skg = api.i8_dense_skg(K, N)
         for mode in (0, 1):
+            skg = api.i8_dense_skg(K, N, mode)
             a8, sa = api.i8_quant(x_d, mode != 0)
             out = torch.empty((M, N), dtype=torch.float16, device=dev)
             work = api.I8Workspace(N, skg, dev)

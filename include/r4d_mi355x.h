@@ -182,6 +182,8 @@ void r4d_i8_pack_w(int64_t wp, int64_t w8, int N, int K, int64_t stream);
 const char* r4d_gemm_i8_dense_check(int M, int K, int N, int SKG);
 size_t r4d_gemm_i8_dense_ws_bytes(int M, int N, int SKG);
 int r4d_mi355x_i8_skg(int K, int N);
+/* No reference counterpart: the dense GEMM's SKG by scale mode (0 = stream-K for the per-128 modes). */
+int r4d_mi355x_i8_dense_skg(int K, int N, int scale_mode);
 
 /* ---- int8 x int8 trellis prefill GEMM (r4d.h:456-521) ---------------------------------------- */
 /* r4d.h:490-492: the weight scale table SW [K/128][N] fp32 (s_eff = 1 / rs, rs = f16(min(1 / s, 60000)),

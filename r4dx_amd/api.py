@@ -288,8 +288,9 @@ def i8_pack_w(wp, out=None, stream=None):
     return out
 
 
-def i8_dense_skg(K, N):
-    return lib().r4d_mi355x_i8_skg(K, N)
+def i8_dense_skg(K, N, scale_mode=0):
+    """The dense GEMM's launch form (r4d_mi355x_i8_dense_skg): 0 = stream-K, else the K split."""
+    return lib().r4d_mi355x_i8_dense_skg(K, N, scale_mode)
 
 
 class I8Workspace:
@@ -306,7 +307,7 @@ def i8_dense_gemm(a8, sa, w8, sw, K, N, scale_mode=0, skg=None, raw=False, out=N
     sums (r4d_gemm_i8_dense_raw)."""
     L = lib()
     M = 256
-    skg = i8_dense_skg(K, N) if skg is None else skg
+    skg = i8_dense_skg(K, N, scale_mode) if skg is None else skg
     msg = L.r4d_gemm_i8_dense_check(M, K, N, skg)
     if msg:
         raise ValueError(msg.decode())

@@ -746,6 +746,13 @@ int r4d_mi355x_i8_skg(int K, int N) {
   return best;
 }
 
+// This build's launch form for the dense int8 GEMM by scale mode: the per-128 modes run stream-K (SKG = 0; measured
+// 8-11 % faster than the best split at both config-4 shapes), row / column scales the split above.
+int r4d_mi355x_i8_dense_skg(int K, int N, int scale_mode) {
+  if (K <= 0 || N <= 0 || K % 128 || N % 128) return 1;
+  return scale_mode != 0 ? 0 : r4d_mi355x_i8_skg(K, N);
+}
+
 // r4d.h:490 (K / 128) N floats
 size_t r4d_trellis_i8_wscale_count(int K, int N) { return (size_t)(K / 128) * (size_t)N; }
 // r4d.h:491

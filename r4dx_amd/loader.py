@@ -49,6 +49,7 @@ SIGS = {
     "r4d_gemm_i8_dense_check": (CSTR, [I32] * 4),
     "r4d_gemm_i8_dense_ws_bytes": (SZ, [I32] * 3),
     "r4d_mi355x_i8_skg": (I32, [I32, I32]),
+    "r4d_mi355x_i8_dense_skg": (I32, [I32, I32, I32]),
     "r4d_trellis_i8_wscale_count": (SZ, [I32, I32]),
     "r4d_trellis_i8_wscale": (None, [I64, I64, I32, I32, I32, I64]),
     "r4d_trellis_i8_dump_w": (None, [I64, I64, I64, I64, I32, I32, I32, I64]),

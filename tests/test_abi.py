@@ -160,3 +160,14 @@ def test_parts_wrappers_refuse_before_launch():
         api.trellis_gemm_m256_parts(a256, [0, 512], w, svh, 1024, 512, 4, skg=1)
     with pytest.raises(ValueError, match="gsh"):
         api.trellis_gemm_m64(a[0], w, svh, 1024, 512, 4, skg=1, wq=(svh, 4))
+
+
+def test_dense_i8_plan(L):
+    """The dense int8 launch form: stream-K (0) for the per-128 modes, the K split of r4d_mi355x_i8_skg for row
+    scales; every form passes the dense check."""
+    for K, N in ((5120, 17408), (17408, 5120), (1024, 256)):
+        assert L.r4d_mi355x_i8_dense_skg(K, N, 0) == L.r4d_mi355x_i8_skg(K, N)
+        for mode in (1, 2):
+            assert L.r4d_mi355x_i8_dense_skg(K, N, mode) == 0
+        for mode in (0, 1, 2):
+            assert not L.r4d_gemm_i8_dense_check(256, K, N, L.r4d_mi355x_i8_dense_skg(K, N, mode))
