@@ -44,6 +44,14 @@ __device__ __forceinline__ unsigned ti8_rs_from_s(float s) {
   const unsigned b = __builtin_bit_cast(unsigned short, h);
   return b | (b << 16);
 }
+// The same rs from a table entry s_eff = 1 / rs (fp32) with the hardware reciprocal instead of the IEEE divide: rs is an
+// f16 number in [1, 60000] and s_eff its correctly rounded reciprocal, so 1 / s_eff lies within an fp32 ulp of rs and
+// any result within a few ulps converts back to rs (checked for every normal f16 up to 60000 at +-3 ulps).
+__device__ __forceinline__ unsigned ti8_rs_from_seff(float seff) {
+  const _Float16 h = (_Float16)__builtin_fminf(__builtin_amdgcn_rcpf(seff), 60000.f);
+  const unsigned b = __builtin_bit_cast(unsigned short, h);
+  return b | (b << 16);
+}
 // four f16 weights (two dwords, element order) -> four int8 bytes: low byte of f16(w * rs + 1536)
 __device__ __forceinline__ unsigned ti8_q4(unsigned d0, unsigned d1, unsigned rs2) {
   const r4h2 c = {(_Float16)1536.f, (_Float16)1536.f};
@@ -235,7 +243,7 @@ __device__ __forceinline__ void ti8_piece(const TI8Args& p, unsigned char (*bst)
 #pragma unroll
       for (int cs = 0; cs < 2; ++cs) {
         const int nl = 32 * (wave & 3) + 16 * dt + 8 * cs + dc;
-        const unsigned rs2 = SC == kSBlk ? ti8_rs_from_s(dsw[cs]) : rsc[cs];
+        const unsigned rs2 = SC == kSBlk ? ti8_rs_from_seff(dsw[cs]) : rsc[cs];
         const r4u4 v = {ti8_q4(d[cs][0][0], d[cs][0][1], rs2), ti8_q4(d[cs][0][2], d[cs][0][3], rs2),
                         ti8_q4(d[cs][1][0], d[cs][1][1], rs2), ti8_q4(d[cs][1][2], d[cs][1][3], rs2)};
         *(r4u4*)&bst[st & 1][dq][ti8_bslot(nl)][0] = v;
@@ -313,7 +321,8 @@ __device__ __forceinline__ void ti8_piece(const TI8Args& p, unsigned char (*bst)
     for (int ct = 0; ct < 8; ++ct) {
       const r4i4 b = *(const r4i4*)(stg + ti8_bslot(16 * ct + r16) * 16);
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii) iacc[ii][ct] = mfma_i8(a[ii], b, iacc[ii][ct]);
+      for (int ii = 0; ii < 2; ++ii)   // per-128: a block's first step starts its int32 sums from 0 (the MFMA's C)
+        iacc[ii][ct] = mfma_i8(a[ii], b, (BLKA && !odd) ? (r4i4){0, 0, 0, 0} : iacc[ii][ct]);
     }
     if constexpr (BLKA) {
       if (odd) {   // the 128-k block is complete: acc += float(int32) * scale
@@ -325,7 +334,6 @@ __device__ __forceinline__ void ti8_piece(const TI8Args& p, unsigned char (*bst)
             for (int j = 0; j < 4; ++j) {
               const float sc = SC == kSBlk ? s.sa[ii][j] * s.sw[ct] : s.sa[ii][j];
               facc[ii][ct][j] = __builtin_fmaf((float)iacc[ii][ct][j], sc, facc[ii][ct][j]);
-              iacc[ii][ct][j] = 0;
             }
       }
     }
