@@ -42,6 +42,9 @@ def parse():
     ap.add_argument("--pmc-prefill", action="store_true",
                     help="counter pass for the prefill kernels: each config-2 M = 256 shape, then the config-4 "
                          "dense and trellis int8 GEMMs, launched twice each; prints the launch order, no JSON line")
+    ap.add_argument("--pmc-dense-forms", action="store_true",
+                    help="counter pass for the dense int8 launch forms: 5120 x 17408 row scales, three eager launches "
+                         "at SKG 1, then three in stream-K; prints no JSON line")
     ap.add_argument("--pmc", action="store_true",
                     help="counter pass for rocprofv3 --pmc: a 512 MiB copy (calibration) and two eager "
                          "passes of the GEMV launches; prints no JSON line")
@@ -62,6 +65,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.pmc_prefill:
         pmc_prefill(api, WL, args.kb)
+        return
+    if args.pmc_dense_forms:
+        pmc_dense_forms(api, WL)
         return
     KB, M = args.kb, args.m
     shapes = WL.LAYER_SHAPES
@@ -420,6 +426,25 @@ def bench_config1_rows(api, WL, reps=4):
         torch.cuda.empty_cache()
     return {"workload": "config 1 layer, 6 launch groups; two_launch = transforms + parts GEMVs, fused = "
                         "r4dx_trellis_gemv_xf_parts; mix = GDN and attention at KB 5, MLP at KB 4", "rows": rows}
+
+
+def pmc_dense_forms(api, WL):
+    """The dense int8 GEMM at 5120 x 17408 (row scales) in its two launch forms, three eager launches each on one
+    weight copy: SKG 1 (136 workgroups), then stream-K (256)."""
+    import torch
+    dev = torch.device("cuda:0")
+    K, N = 5120, 17408
+    x, w8, sw = WL.int8_case(K, N, 3)
+    w_d = api.i8_pack_w(torch.from_numpy(w8).to(dev))
+    sw_d = torch.from_numpy(sw).to(dev)
+    a8, sa = api.i8_quant(torch.from_numpy(x.view("int16")).to(dev), False)
+    out = torch.empty((256, N), dtype=torch.float16, device=dev)
+    for skg in (1, 0):
+        work = api.I8Workspace(N, skg, dev)
+        for _ in range(3):
+            api.i8_dense_gemm(a8, sa, w_d, sw_d, K, N, scale_mode=0, skg=skg, out=out, work=work)
+        torch.cuda.synchronize()
+    print(json.dumps({"pmc_pass": "done", "launch_order": ["skg1"] * 3 + ["stream-K"] * 3}), flush=True)
 
 
 def pmc_prefill(api, WL, KB):
