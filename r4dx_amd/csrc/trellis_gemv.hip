@@ -132,11 +132,11 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
   const int nst = max(0, min(nsw, steps_all - st_beg));
   const int ktl_pad = SK * nsw * 4;            // k-tiles the LDS copy of A covers (zero past ktw)
 
-  // LDS: [A slice (ALDS) + zero block] [SK - 1 partial accumulators per pair] [M x 128 sums]
-  //      [8 x 4 x 128 reduce runs] [flag]
-  const size_t a_vec = ALDS ? (size_t)ktl_pad * M * 2 + 2 : 0;      // r4u4 units
+  // LDS: the A slice (ALDS) + its zero block while the k loop runs; after it (every wave past the barrier that ends
+  // the loop), the same bytes hold [SK - 1 partial accumulators per pair] [M x 128 sums] [8 x 4 x 128 reduce runs]
+  // [flag]. The launch asks for the larger of the two.
   r4u4* alds = lds_raw;
-  float* part_acc = (float*)(lds_raw + a_vec);                       // [(SK-1) * NPW][8 MT][64]
+  float* part_acc = (float*)lds_raw;                                 // [(SK-1) * NPW][8 MT][64]
   float* red = part_acc + (size_t)(SK - 1) * NPW * 8 * MT * 64;      // [M][128]
   float* runs = red + (size_t)M * 128;                               // [8][4][128]
   const int red_rows = min(kRedRows, M);      // rows per finish pass (the LDS holds no more)
@@ -340,6 +340,8 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
       if (st + i < nst) compute(ring[i], st + i);
   }
 
+  // The A slice is dead once every wave has left the loop: the combine, the sums and the reduce runs reuse its bytes.
+  if constexpr (ALDS) __syncthreads();
   // Combine the SK waves of each pair in k order (ks = 0, 1, ...) into wave ks = 0.
   if constexpr (SK > 1) {
     if (ks > 0) {
@@ -560,9 +562,13 @@ __global__ __launch_bounds__(256) void tq_wscale_kernel(const unsigned* __restri
 
 // Dynamic LDS of one launch.
 size_t gemv_ktl_pad(int SK, int ktw) { return (size_t)SK * ((((ktw + 3) >> 2) + SK - 1) / SK) * 4; }
+// The A slice (ALDS) and, after the k loop, in the same bytes: the partial accumulators, the sums, the reduce runs and
+// the flag.
 size_t gemv_lds(int MT, int NPW, int SK, bool alds, int ktw, int M) {
-  return (alds ? gemv_ktl_pad(SK, ktw) * M * 32 + 32 : 0) + (size_t)(SK - 1) * NPW * 8 * MT * 64 * 4 +
-         (size_t)(M + kRedParts * (M < kRedRows ? M : kRedRows)) * 128 * 4 + 16;
+  const size_t a = alds ? gemv_ktl_pad(SK, ktw) * M * 32 + 32 : 0;
+  const size_t tail = (size_t)(SK - 1) * NPW * 8 * MT * 64 * 4 +
+                      (size_t)(M + kRedParts * (M < kRedRows ? M : kRedRows)) * 128 * 4 + 16;
+  return a > tail ? a : tail;
 }
 constexpr size_t kAldsMax = 48 * 1024;   // A slices up to this many bytes are staged in LDS
 
