@@ -89,6 +89,16 @@ __device__ __forceinline__ void load_words_ptr(Words<KB>& s, const unsigned* __r
 constexpr int kRedParts = 8;         // the final slice sum is 8 interleaved runs, added in order
 constexpr int kRedRows = 4;          // rows of the final slice sum per pass (8 measured slower at M = 8: LDS)
 
+// n / d for the staging loops' row split (d = M <= 64, n below 2^20): one high multiply by the launch-uniform
+// floor(2^32 / d) + 1, exact whenever n d < 2^32 (the error term n e / (d 2^32), 0 < e <= d, stays below 1 / d);
+// d = 1 (whose multiplier would need 33 bits) is marked by 0 and returns n.
+__device__ __forceinline__ unsigned r4_div_magic(unsigned d) {
+  return d == 1u ? 0u : (unsigned)(0x100000000ull / d) + 1u;
+}
+__device__ __forceinline__ int r4_div_by(int n, unsigned magic) {
+  return magic ? (int)__umulhi((unsigned)n, magic) : n;
+}
+
 // XF > 0: A0 is the raw input x [M][K] (XF 1: f16, 2: bf16) and the workgroup stages its own slice of the
 // transformed A = f16(FWHT128(fp32(x) * suh) * xscale) (suh of the group's column part) straight into LDS --
 // the arithmetic of r4dx_trellis_input_*, so A is bit-identical to the unfused path's.
@@ -131,6 +141,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
   const int st_beg = ks * nsw;
   const int nst = max(0, min(nsw, steps_all - st_beg));
   const int ktl_pad = SK * nsw * 4;            // k-tiles the LDS copy of A covers (zero past ktw)
+  const unsigned mmag = r4_div_magic((unsigned)M);
 
   // LDS: the A slice (ALDS) + its zero block while the k loop runs; after it (every wave past the barrier that ends
   // the loop), the same bytes hold [SK - 1 partial accumulators per pair] [M x 128 sums] [8 x 4 x 128 reduce runs]
@@ -240,7 +251,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
   };
   auto xf_load = [&](int u) {
     XfIn v = {0u, (r4f2){0.f, 0.f}};
-    const int b = u / M, r = u - b * M;
+    const int b = r4_div_by(u, mmag), r = u - b * M;
     if (u < xf_nblk * M && 8 * b < ktw) {
       const size_t kb = (size_t)16 * kt0 + 128 * (size_t)b + 2 * lane;
       v.x2 = *(const unsigned*)(A0 + (size_t)r * K + kb);
@@ -266,7 +277,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     // chunk (h = 0: k 0-3, 8-11; h = 1: k 4-7, 12-15); then the zero block.
     unsigned* ah = (unsigned*)alds;
     auto xf_stage = [&](int u, const XfIn& v) {
-      const int b = u / M, r = u - b * M;
+      const int b = r4_div_by(u, mmag), r = u - b * M;
       if (u >= xf_nblk * M) return;
       unsigned hv = 0u;
       if (8 * b < ktw) {
@@ -297,7 +308,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
       const int i = threadIdx.x;
       if (i < chunks + 2) {
         r4u4 v = {0u, 0u, 0u, 0u};
-        const int j = i & 1, rm = i >> 1, r = rm % M, ktl = rm / M;
+        const int j = i & 1, rm = i >> 1, ktl = r4_div_by(rm, mmag), r = rm - ktl * M;
         if (i < chunks && ktl < ktw) v = *(const r4u4*)(A + (size_t)r * K + 16 * (kt0 + ktl) + 8 * j);
         r4u2* dst = (r4u2*)(alds + (size_t)rm * 2);
         dst[j] = (r4u2){v[0], v[1]};
@@ -308,7 +319,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
 #pragma unroll
       for (int u = 0; u < kStageU; ++u) {
         const int i = i0 + u * NT;
-        const int j = i & 1, rm = i >> 1, r = rm % M, ktl = rm / M;
+        const int j = i & 1, rm = i >> 1, ktl = r4_div_by(rm, mmag), r = rm - ktl * M;
         v[u] = (r4u4){0u, 0u, 0u, 0u};
         if (i < chunks && ktl < ktw) v[u] = *(const r4u4*)(A + (size_t)r * K + 16 * (kt0 + ktl) + 8 * j);
       }
