@@ -3,7 +3,8 @@
 // std::runtime_error the reference's contract promises (third_party/libr4d/r4d.h:30-31), and results checked
 // against the CPU oracle (oracle/r4o.h, test infrastructure). The checks follow the reference's
 // tests/kernels/test_trellis_gemm.cpp: bit-exact dequant, the transform, the GEMV's sums and epilogue, the split's
-// tickets after a poisoned buffer, and the M = 256 / M = 64 row identity.
+// tickets after a poisoned buffer, and the M = 256 / M = 64 row identity; then the w4a16 GEMM (quant_int4.hpp's
+// packers), the row argmax (argmax_ref.hpp's order), the int8 row quantizer and the dense int8 GEMM's exact sums.
 //
 //   engine_abi cpu   checks that need no GPU (the _check rules, the thrown errors, the sizes)
 //   engine_abi gpu   all of them, on device 0
@@ -207,6 +208,85 @@ void gpu_checks() {
     same = same && std::memcmp(c64.data(), c256.data() + (size_t)r0 * N, c64.size() * 2) == 0;
   }
   expect(same, "M = 256 rows == M = 64 rows at SK 1, SKG 2, bit for bit");
+
+  // 6. w4a16 at group 64 (quant_int4.hpp's quantizer and packers), then the argmax of its fp32 logits
+  {
+    const int WN = 512, WK = 512, G = 64, WM = 2;
+    std::vector<float> wf((size_t)WN * WK), sc((size_t)WN * WK / G);
+    for (auto& v : wf) v = 0.05f * gauss();
+    std::vector<uint8_t> q4((size_t)WN * WK), z((size_t)WN * WK / G);
+    r4o_w4_quantize(wf.data(), WN, WK, G, q4.data(), sc.data(), z.data());
+    std::vector<uint32_t> wq((size_t)WN * WK / 8), wsz((size_t)WN / 16 * (WK / G) * 16);
+    r4o_w4_pack(q4.data(), WN, WK, wq.data());
+    r4o_w4_pack_scales(sc.data(), z.data(), WN, WK, G, wsz.data());
+    std::vector<uint16_t> a4((size_t)WM * WK);
+    for (auto& v : a4) v = r4o_f32_to_f16(gauss());
+    Dev dwq(wq.size() * 4), dwsz(wsz.size() * 4), da4(a4.size() * 2), dc4((size_t)WM * WN * 2);
+    dwq.put(wq);
+    dwsz.put(wsz);
+    da4.put(a4);
+    expect(r4d_gemm_w4a16_nt_m64_check(G, WM, WK, WN) == nullptr, "w4a16 check accepts g64 M 2");
+    r4d_gemm_w4a16_nt_m64_g(G, da4.a(), dwq.a(), dwsz.a(), dc4.a(), WM, WK, WN, 0, 0, 0, 0, 0, s);
+    HIPCHECK(hipStreamSynchronize(st));
+    const std::vector<uint16_t> c4 = dc4.get<uint16_t>((size_t)WM * WN);
+    std::vector<double> y((size_t)WM * WN);
+    r4o_w4_gemm_ref(a4.data(), wq.data(), wsz.data(), WM, WN, WK, G, y.data(), 1);
+    double yms = 0, wst = 0;
+    for (double v : y) yms += v * v;
+    const double yrms = std::sqrt(yms / y.size());
+    for (size_t i = 0; i < y.size(); ++i)
+      wst = std::fmax(wst, std::fabs(r4o_bf16_to_f32(c4[i]) - y[i]) / (std::ldexp(std::fabs(y[i]), -8) + 1e-3 * yrms));
+    expect(wst <= 1.0, "w4a16 bf16 within one bf16 rounding of the fp64 reference (worst " + std::to_string(wst) + ")");
+
+    // argmax over fp32 rows (ties to the lowest index, NaN never wins), against the oracle's order
+    const int R = 3, V = 100003;
+    std::vector<float> lg((size_t)R * V);
+    for (auto& v : lg) v = gauss();
+    lg[5] = 40.f;
+    lg[V + 77] = 40.f;
+    lg[V + 99] = 40.f;                                   // a tie: the lower index wins
+    lg[2 * (size_t)V + 11] = std::nanf("");
+    Dev dl(lg.size() * 4), di(R * 4), dv(R * 4);
+    dl.put(lg);
+    r4dx_argmax_rows_f32(dl.a(), V, di.a(), dv.a(), 1, R, V, s);
+    HIPCHECK(hipStreamSynchronize(st));
+    const std::vector<int32_t> idx = di.get<int32_t>(R);
+    bool am = true;
+    for (int r = 0; r < R; ++r) {
+      float bv = 0.f;
+      am = am && idx[r] == r4o_argmax_f32(lg.data() + (size_t)r * V, V, &bv);
+    }
+    expect(am, "argmax rows == the oracle's order (ties, NaN)");
+  }
+
+  // 7. int8: the per-row activation quantizer byte for byte, and the dense GEMM's exact int32 sums
+  {
+    const int IM = 256, IK = 512, IN = 256;
+    std::vector<uint16_t> xi((size_t)IM * IK);
+    for (auto& v : xi) v = r4o_f32_to_f16(gauss());
+    std::vector<float> sa_ref(IM);
+    std::vector<int8_t> ap((size_t)IM * IK), a8_ref((size_t)IM * IK);
+    r4o_i8_quant_act_row(xi.data(), IM, IK, sa_ref.data(), ap.data());
+    r4o_pack_a8(ap.data(), IK, a8_ref.data());
+    Dev dxi(xi.size() * 2), da8((size_t)IM * IK), dsa(IM * 4);
+    dxi.put(xi);
+    r4d_trellis_i8_quant_act_row(dxi.a(), da8.a(), dsa.a(), 1, 0, IK, s);
+    HIPCHECK(hipStreamSynchronize(st));
+    const std::vector<int8_t> a8 = da8.get<int8_t>((size_t)IM * IK);
+    const std::vector<float> sa = dsa.get<float>(IM);
+    expect(a8 == a8_ref && std::memcmp(sa.data(), sa_ref.data(), IM * 4) == 0,
+           "int8 row quantizer == oracle (A8 bytes and scales)");
+    std::vector<int8_t> wp((size_t)IN * IK);
+    for (auto& v : wp) v = (int8_t)((int)(rnd() % 255) - 127);
+    Dev dwp(wp.size()), dw8(wp.size()), dci((size_t)IM * IN * 4);
+    dwp.put(wp);
+    r4d_i8_pack_w(dwp.a(), dw8.a(), IN, IK, s);
+    r4d_gemm_i8_dense_raw(da8.a(), dw8.a(), dci.a(), 0, 0, IM, IK, IN, 1, s);
+    HIPCHECK(hipStreamSynchronize(st));
+    std::vector<int32_t> acc((size_t)IM * IN);
+    r4o_i8_gemm_i32(ap.data(), wp.data(), IM, IN, IK, acc.data(), 1);
+    expect(dci.get<int32_t>((size_t)IM * IN) == acc, "dense int8 int32 sums exact");
+  }
   HIPCHECK(hipStreamDestroy(st));
 }
 
