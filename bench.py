@@ -281,7 +281,10 @@ def main():
     m256 = leg(args.no_m256, bench_m256, api, WL, KB)
     i8 = leg(args.no_i8, bench_int8, api, WL)
     ti8 = leg(args.no_i8, bench_trellis_i8, api, WL, KB)
-    vendor = leg(args.no_vendor, bench_vendor, WL)
+    try:   # context only: a vendor-library failure must not cost the bench line
+        vendor = leg(args.no_vendor, bench_vendor, WL)
+    except Exception as e:  # noqa: BLE001
+        vendor = {"error": f"{type(e).__name__}: {e}"[:300]}
 
     cpu = None
     if not args.no_cpu:
