@@ -203,10 +203,8 @@ void xq_launch(bool row_scale, const R4XSrc& src, int64_t K, int nout, const XqO
     const size_t lds = (size_t)nout * K * 2;
     // the row's values plus the kernel's 48 static bytes must fit the 160 KiB of a workgroup
     if (lds > 160 * 1024 - 256) r4d::fail(entry, "nout K 2 bytes must stay below 160 KiB of LDS");
-    if (lds > 64 * 1024 &&
-        hipFuncSetAttribute((const void*)xq_row_kernel<SRC>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-            hipSuccess)
-      r4d::fail(entry, "hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
+    static std::atomic<unsigned long long> lds_set{0};
+    if (lds > 64 * 1024) r4d::allow_lds((const void*)xq_row_kernel<SRC>, lds_set, entry);
     hipLaunchKernelGGL((xq_row_kernel<SRC>), dim3(256), dim3(256), lds, st, src, (int)K, nout, p, scale);
   } else {
     const long long waves = 256LL * (K / 128);

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <stdexcept>
 #include <string>
 
@@ -31,6 +32,17 @@ inline void require(const char* entry, const std::string& msg) {
 inline void launch_ok(const char* entry) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) fail(entry, std::string("launch failed: ") + hipGetErrorString(e));
+}
+// Lets kernel `fn` take up to 160 KiB of dynamic LDS on the current device (the attribute is per device): set once
+// per device and kernel (`done` holds a bit per device, 64 at most), a failure thrown naming `entry`.
+inline void allow_lds(const void* fn, std::atomic<unsigned long long>& done, const char* entry) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) fail(entry, "no usable current device");
+  const unsigned long long bit = 1ull << dev;
+  if (done.load(std::memory_order_acquire) & bit) return;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+    fail(entry, "hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
+  done.fetch_or(bit, std::memory_order_acq_rel);
 }
 inline bool pow2_in(int v, int lo, int hi) {
   return v >= lo && v <= hi && (v & (v - 1)) == 0;

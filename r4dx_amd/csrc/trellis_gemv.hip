@@ -131,7 +131,6 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
   const int group = (blockIdx.x * NPW) >> 2;
   const int KT = K >> 4, ktw = KT / SKG, kt0 = ky * ktw;
   const unsigned short* __restrict__ A0 = ap.a[0];
-  const int n_split = ap.n_end[0];
   const unsigned short* __restrict__ A = r4_part_a(ap, group * 128);
   const int q = lane >> 4, t = (lane >> 3) & 1, c = lane & 7, mrow = lane & 15;
 
@@ -611,12 +610,9 @@ void launch_gemv(const r4d_gemv_args& a) {
   const int ktw = a.K / 16 / a.SKG;
   const size_t smem = gemv_lds(MT, NPW, SK, ALDS, ktw, a.M);
   if (smem > 160 * 1024) r4d::fail("gemm_trellis_nt_m64", "LDS request above 160 KiB");
-  static bool attr = false;
-  if (!attr && smem > 64 * 1024) {
-    (void)hipFuncSetAttribute((const void*)tq_gemv_kernel<KB, MT, NPW, SK, ALDS, XF, WQ>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    attr = true;
-  }
+  static std::atomic<unsigned long long> lds_set{0};
+  if (smem > 64 * 1024)
+    r4d::allow_lds((const void*)tq_gemv_kernel<KB, MT, NPW, SK, ALDS, XF, WQ>, lds_set, "gemm_trellis_nt_m64");
   const R4AParts ap = r4_parts((const void*)a.a0, (const void*)a.a1, a.n_split, (const void*)a.a2, a.n_end1,
                                (const void*)a.a3, a.n_end2);
   R4SParts sp;

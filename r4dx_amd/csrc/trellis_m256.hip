@@ -141,7 +141,7 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
       poisoned = *(volatile int*)lds != 0;                                                                 \
       __syncthreads();                                                                                     \
     }                                                                                                      \
-    (void)poisoned; (void)A; (void)Kv; (void)Nv;
+    (void)poisoned; (void)A; (void)Kv; (void)Nv; (void)kt0;
 
   if (wave >= 4) {
    for (int si = 0; si < sh.nseg; ++si) {
@@ -550,12 +550,8 @@ void m256_launch_rt(const R4AParts& ap, const unsigned* w,
                     const float* svh, void* c, float* ws, unsigned* tickets, int M, int K, int N, int SKG, int full,
                     float out_scale, const float* wsc, int wq_gsh, hipStream_t st) {
   constexpr unsigned lds = 2 * (32 * RT * 128 + 128 * 128);
-  static bool attr = false;
-  if (!attr) {
-    (void)hipFuncSetAttribute((const void*)tq_m256_kernel<KB, RT, WQ>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)lds);
-    attr = true;
-  }
+  static std::atomic<unsigned long long> lds_set{0};
+  r4d::allow_lds((const void*)tq_m256_kernel<KB, RT, WQ>, lds_set, "gemm_trellis_nt_m256");
   const int P = m256_balanced_p(M, N, SKG, ws != nullptr, tickets != nullptr);
   // the published accumulators follow the SKG slices in ws (SKG = 1: no slices, they start at ws)
   float* fix = ws ? ws + (SKG > 1 ? (size_t)SKG * M * N : 0) : nullptr;
