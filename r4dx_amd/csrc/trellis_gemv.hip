@@ -263,12 +263,17 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
 #pragma unroll
     for (int j = 0; j < kXfPre; ++j) xpre[j] = xf_load(wave + NW * j);
   }
-  // The weight stream starts before A is staged, so its latency overlaps the staging.
+  // The weight stream starts while A is staged, so its latency overlaps the staging. In the plain staged form the
+  // first pass's A loads go out just before it: loads retire in order, so the staging then waits for A only, not for
+  // the PF steps of weights behind it.
   St ring[PF];
-  if (nst > 0) {
+  // unconditional (a wave without steps reads past its buffer, which returns 0), so no branch joins the loads and the
+  // staging's waits count the A loads only
+  auto load_ring = [&]() {
 #pragma unroll
     for (int i = 0; i < PF; ++i) load(ring[i], i);
-  }
+  };
+  if constexpr (!(ALDS && XF == 0)) load_ring();
   if constexpr (ALDS && XF > 0) {
     // A = f16(FWHT128(fp32(x) * suh) * xscale) (r4_fwht128_wave_pairs: the same fp32 operations per element
     // as r4dx_trellis_input_*), each lane's two adjacent k written as one dword to its fragment slot --
@@ -303,34 +308,53 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     // per pass, not one per chunk (at M = 8 and up a workgroup stages several chunks per thread)
     constexpr int kStageU = 4;
     const int chunks = ktl_pad * M * 2;
+    // chunk i's byte offset in A, or one past the buffer (a zero chunk): the loads are unconditional buffer loads, so
+    // the kStageU of a pass go out back to back (a load under a branch waits for its data at the branch's end)
+    auto chunk_off = [&](int i) -> unsigned {
+      const int j = i & 1, rm = i >> 1, ktl = r4_div_by(rm, mmag), r = rm - ktl * M;
+      return (i < chunks && ktl < ktw) ? (unsigned)(((size_t)r * K + 16 * (kt0 + ktl) + 8 * j) * 2) : 0xFFFFFFF0u;
+    };
+    auto chunk_load = [&](int i) -> r4u4 {
+      return __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(ar, chunk_off(i), 0, 0));
+    };
     if (chunks + 2 <= NT) {   // one chunk per thread at most (M = 1, 2): no unrolled address arithmetic
       const int i = threadIdx.x;
+      const int j = i & 1, rm = i >> 1;
+      const r4u4 v = chunk_load(i);
+      __builtin_amdgcn_sched_barrier(0);   // the A load goes out before the weight loads
+      load_ring();
       if (i < chunks + 2) {
-        r4u4 v = {0u, 0u, 0u, 0u};
-        const int j = i & 1, rm = i >> 1, ktl = r4_div_by(rm, mmag), r = rm - ktl * M;
-        if (i < chunks && ktl < ktw) v = *(const r4u4*)(A + (size_t)r * K + 16 * (kt0 + ktl) + 8 * j);
         r4u2* dst = (r4u2*)(alds + (size_t)rm * 2);
         dst[j] = (r4u2){v[0], v[1]};
         dst[2 + j] = (r4u2){v[2], v[3]};
       }
-    } else for (int i0 = threadIdx.x; i0 < chunks + 2; i0 += kStageU * NT) {
-      r4u4 v[kStageU];
+    } else {
+      // every thread runs the first pass (chunks + 2 > NT here): its loads, then the weight stream, unconditionally, so
+      // the waits before the writes count the A loads only
+      // branch-free writes: a chunk past the copy is zero (its load read past the buffer) and lands in the zero block
+      auto put_pass = [&](int i0, const r4u4 (&v)[kStageU]) {
 #pragma unroll
-      for (int u = 0; u < kStageU; ++u) {
-        const int i = i0 + u * NT;
-        const int j = i & 1, rm = i >> 1, ktl = r4_div_by(rm, mmag), r = rm - ktl * M;
-        v[u] = (r4u4){0u, 0u, 0u, 0u};
-        if (i < chunks && ktl < ktw) v[u] = *(const r4u4*)(A + (size_t)r * K + 16 * (kt0 + ktl) + 8 * j);
-      }
-#pragma unroll
-      for (int u = 0; u < kStageU; ++u) {
-        const int i = i0 + u * NT;
-        if (i < chunks + 2) {
-          const int j = i & 1, rm = i >> 1;
+        for (int u = 0; u < kStageU; ++u) {
+          const int i = i0 + u * NT;
+          const int j = i & 1, rm = min(i >> 1, chunks >> 1);
           r4u2* dst = (r4u2*)(alds + (size_t)rm * 2);
           dst[j] = (r4u2){v[u][0], v[u][1]};        // h = 0, elements 4j .. 4j + 3
           dst[2 + j] = (r4u2){v[u][2], v[u][3]};    // h = 1
         }
+      };
+      {
+        r4u4 v[kStageU];
+#pragma unroll
+        for (int u = 0; u < kStageU; ++u) v[u] = chunk_load((int)threadIdx.x + u * NT);
+        __builtin_amdgcn_sched_barrier(0);
+        load_ring();
+        put_pass((int)threadIdx.x, v);
+      }
+      for (int i0 = (int)threadIdx.x + kStageU * NT; i0 < chunks + 2; i0 += kStageU * NT) {
+        r4u4 v[kStageU];
+#pragma unroll
+        for (int u = 0; u < kStageU; ++u) v[u] = chunk_load(i0 + u * NT);
+        put_pass(i0, v);
       }
     }
     __syncthreads();
