@@ -248,14 +248,17 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     unsigned x2;   // x[2l], x[2l + 1] (f16 or bf16 bits)
     r4f2 s2;       // suh[2l], suh[2l + 1]
   };
+  // unconditional buffer loads (a unit past the slice reads past both buffers and gets 0): no branch around a load,
+  // so the waits before a unit's use count only what is needed
+  const r4_rsrc xr = r4_make_rsrc(A0, (unsigned)((size_t)M * K * 2));
+  const r4_rsrc shr = r4_make_rsrc(suh_p, (unsigned)((size_t)K * 4));
   auto xf_load = [&](int u) {
-    XfIn v = {0u, (r4f2){0.f, 0.f}};
+    XfIn v;
     const int b = r4_div_by(u, mmag), r = u - b * M;
-    if (u < xf_nblk * M && 8 * b < ktw) {
-      const size_t kb = (size_t)16 * kt0 + 128 * (size_t)b + 2 * lane;
-      v.x2 = *(const unsigned*)(A0 + (size_t)r * K + kb);
-      v.s2 = *(const r4f2*)(suh_p + kb);
-    }
+    const bool ok = u < xf_nblk * M && 8 * b < ktw;
+    const unsigned kb = (unsigned)(16 * kt0 + 128 * b + 2 * lane);
+    v.x2 = __builtin_amdgcn_raw_buffer_load_b32(xr, ok ? ((unsigned)r * (unsigned)K + kb) * 2u : 0xFFFFFFF0u, 0, 0);
+    v.s2 = __builtin_bit_cast(r4f2, __builtin_amdgcn_raw_buffer_load_b64(shr, ok ? kb * 4u : 0xFFFFFFF0u, 0, 0));
     return v;
   };
   XfIn xpre[XF > 0 ? kXfPre : 1];
@@ -298,7 +301,13 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
 #pragma unroll
     for (int j = 0; j < kXfPre; ++j) xf_stage(wave + NW * j, xpre[j]);
 #pragma unroll 1
-    for (int u = wave + NW * kXfPre; u < xf_nblk * M; u += NW) xf_stage(u, xf_load(u));
+    for (int u0 = wave + NW * kXfPre; u0 < xf_nblk * M; u0 += NW * kXfPre) {   // the rest, kXfPre units per round trip
+      XfIn v[kXfPre];
+#pragma unroll
+      for (int j = 0; j < kXfPre; ++j) v[j] = xf_load(u0 + NW * j);
+#pragma unroll
+      for (int j = 0; j < kXfPre; ++j) xf_stage(u0 + NW * j, v[j]);
+    }
     if (threadIdx.x < 8) ah[(size_t)ktl_pad * M * 8 + threadIdx.x] = 0u;
     __syncthreads();
   } else if constexpr (ALDS) {
