@@ -28,15 +28,26 @@ __global__ __launch_bounds__(64) void tq_input_kernel(R4XSrc src, int64_t K, int
   const int64_t row = blockIdx.y;
   const float x0 = r4_xsrc<SRC, BF16>(src, row, k0 + lane);
   const float x1 = r4_xsrc<SRC, BF16>(src, row, k0 + lane + 64);
+  // every output's suh requested up front (an absent output reads the first one's): one memory round trip for the
+  // wave instead of one per output
+  float s0[kMaxOut], s1[kMaxOut];
 #pragma unroll
   for (int o = 0; o < kMaxOut; ++o) {
-    if (o >= nout) break;
-    float v0 = x0 * p.suh[o][k0 + lane];
-    float v1 = x1 * p.suh[o][k0 + lane + 64];
+    const float* sp = p.suh[o < nout ? o : 0];
+    s0[o] = sp[k0 + lane];
+    s1[o] = sp[k0 + lane + 64];
+  }
+  // every output computed (an absent one's work is discarded), so the loads above stay ahead of all of it
+#pragma unroll
+  for (int o = 0; o < kMaxOut; ++o) {
+    float v0 = x0 * s0[o];
+    float v1 = x1 * s1[o];
     r4_fwht128_wave(v0, v1, lane);
-    unsigned short* dst = p.out[o] + row * K + k0;
-    dst[lane] = r4_f16_rn(v0 * scale);
-    dst[lane + 64] = r4_f16_rn(v1 * scale);
+    if (o < nout) {
+      unsigned short* dst = p.out[o] + row * K + k0;
+      dst[lane] = r4_f16_rn(v0 * scale);
+      dst[lane + 64] = r4_f16_rn(v1 * scale);
+    }
   }
 }
 
