@@ -475,6 +475,41 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
     // and returns 0, so every thread issues all loads of its kFinItems items at once, with no branches.
     const unsigned sy4 = (unsigned)M * (unsigned)N * 4u;
     const r4_rsrc wsr = r4_make_rsrc(ws, (unsigned)SKG * sy4);
+    if (SKG <= kRedParts) {
+      // At most one slice per run (every planned split): each thread sums whole elements -- run p is 0.f + slice p,
+      // the runs are added in order and the empty ones (p >= SKG) add +0.f, which the one addition below stands for
+      // (adding +0.f again changes nothing) -- with its SKG loads issued at once: the same bits as the general form
+      // below, without its loads of absent slices and its second pass through LDS.
+      constexpr int kFinE = 2;   // elements per thread per pass
+      for (int e0 = (int)threadIdx.x; e0 < M * 128; e0 += kFinE * NT) {
+        float tv[kFinE][kRedParts];
+#pragma unroll
+        for (int it = 0; it < kFinE; ++it) {
+          const int e = e0 + it * NT;
+          const unsigned off = e < M * 128 ? ((unsigned)(e >> 7) * (unsigned)N + (unsigned)(n0 + (e & 127))) * 4u : 0xFFFFFFF0u;
+#pragma unroll
+          for (int p = 0; p < kRedParts; ++p)
+            if (p < SKG)
+              tv[it][p] = __builtin_bit_cast(
+                  float, __builtin_amdgcn_raw_buffer_load_b32(wsr, off == 0xFFFFFFF0u ? off : off + (unsigned)p * sy4, 0, 16));
+        }
+#pragma unroll
+        for (int it = 0; it < kFinE; ++it) {
+          const int e = e0 + it * NT;
+          float v = 0.f + tv[it][0];
+#pragma unroll
+          for (int p = 1; p < kRedParts; ++p)
+            if (p < SKG) v += 0.f + tv[it][p];
+          if (SKG < kRedParts) v += 0.f;
+          if (e < M * 128) {
+            if (full) red[e] = v;
+            else Cf[(size_t)(e >> 7) * N + n0 + (e & 127)] = v;
+          }
+        }
+      }
+      __syncthreads();
+      if (!full) return;
+    } else {
     constexpr int kFinItems = 4;
     for (int r0 = 0; r0 < M; r0 += red_rows) {
       const int rows = min(red_rows, M - r0);
@@ -517,6 +552,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
       __syncthreads();
     }
     if (!full) return;
+    }
   }
   // The epilogue: one wave per row, the group's 128 sums as (lane, lane + 64).
   const float sv0 = svh[n0 + lane], sv1 = svh[n0 + lane + 64];
