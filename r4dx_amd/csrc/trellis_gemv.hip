@@ -1005,6 +1005,15 @@ int r4d_mi355x_trellis_gemv_skg(int K, int N, int KB) {
       best_d = dist;
     }
   }
+  // A pick that leaves 2.25-3.75 workgroups per CU (the M = 1 form: one per pair and slice) ends with a quarter
+  // to three quarters of the CUs running one more workgroup than the rest; the next split, if each wave keeps
+  // >= 12 k-tiles, spreads the work more evenly (6144x5120: SKG 4 -> 8 measured 9.7 -> 9.1 us at M = 1,
+  // 13.0 -> 11.8 us at M = 8).
+  if (best && best < 8 && KT % (2 * best) == 0 && KT / (2 * best) >= 48) {
+    const double per_cu = (double)(N / 32) * best / cus;
+    const double frac = per_cu - (long long)per_cu;
+    if (per_cu >= 2.0 && per_cu < 4.0 && frac >= 0.25 && frac <= 0.75) best *= 2;
+  }
   return best ? best : fallback;
 }
 
