@@ -1005,16 +1005,20 @@ int r4d_mi355x_trellis_gemv_skg(int K, int N, int KB) {
       best_d = dist;
     }
   }
-  // A pick that leaves 2.25-3.75 workgroups per CU (the M = 1 form: one per pair and slice) ends with a quarter
-  // to three quarters of the CUs running one more workgroup than the rest; the next split, if each wave keeps
-  // >= 12 k-tiles, spreads the work more evenly (6144x5120: SKG 4 -> 8 measured 9.7 -> 9.1 us at M = 1,
-  // 13.0 -> 11.8 us at M = 8).
-  if (best && best < 8 && KT % (2 * best) == 0 && KT / (2 * best) >= 48) {
-    const double per_cu = (double)(N / 32) * best / cus;
+  // Workgroups per CU at the pick (the M = 1 form: one per pair and slice). Below 1.25 most of the chip idles;
+  // between x.25 and x.75 under 4, a quarter to three quarters of the CUs run one more workgroup than the rest.
+  // The next split then spreads the work more evenly, as long as each wave keeps >= 10 k-tiles. Measured, SKG
+  // before -> after at M = 1 / M = 8 (us): 6144x5120 4 -> 8: 9.7 -> 9.1 / 13.0 -> 11.8; 5120x6144 2 -> 4:
+  // 10.5 -> 9.4 / 12.3 -> 12.0; 5120x10240 2 -> 4: 13.6 -> 12.3 / 18.4 -> 15.6; 5120x1024 4 -> 8: 5.9 -> 5.6 /
+  // 8.6 -> 7.7; 5120x5120 4 -> 8: 9.2 -> 8.6 / 12.1 -> 11.9.
+  int pick = best ? best : fallback;
+  while (pick < 8 && KT % (2 * pick) == 0 && KT / (2 * pick) >= 40) {
+    const double per_cu = (double)(N / 32) * pick / cus;
     const double frac = per_cu - (long long)per_cu;
-    if (per_cu >= 2.0 && per_cu < 4.0 && frac >= 0.25 && frac <= 0.75) best *= 2;
+    if (!(per_cu < 1.25 || (per_cu < 4.0 && frac >= 0.25 && frac <= 0.75))) break;
+    pick *= 2;
   }
-  return best ? best : fallback;
+  return pick;
 }
 
 }  // extern "C"

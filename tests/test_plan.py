@@ -62,18 +62,19 @@ def test_plans_of_the_tp2_rank_shapes(N, K, parts, n0, kb):
 
 
 @pytest.mark.parametrize("K,N", [(5120, 16384), (5120, 8192), (5120, 34816), (6144, 5120), (17408, 5120),
-                                 (5120, 1024), (1024, 512), (8704, 5120), (3072, 5120)])
+                                 (5120, 1024), (1024, 512), (8704, 5120), (3072, 5120), (5120, 6144), (5120, 10240),
+                                 (5120, 5120)])
 def test_gemv_split_planner_rules(K, N):
     """r4d_mi355x_trellis_gemv_skg: a power of two up to 8 dividing K/16 (whole k-tiles per slice; the engine's rows
-    hold no other SKG), at least 12 k-tiles per wave of a slice when any split allows it, and the documented picks on
+    hold no other SKG), at least 10 k-tiles per wave of a slice when any split allows it, and the documented picks on
     the step's launch shapes."""
     from r4dx_amd import api
     skg = api.trellis_gemv_skg(K, N, 4)
     KT = K // 16
     assert KT % skg == 0 and skg in (1, 2, 4, 8)
     if skg > 1:
-        assert KT / skg / 4 >= 12
+        assert KT / skg / 4 >= 10
     want = {(5120, 16384): 2, (5120, 8192): 2, (5120, 34816): 2, (6144, 5120): 8, (17408, 5120): 8,
-            (5120, 1024): 4, (1024, 512): 1}
+            (5120, 1024): 8, (1024, 512): 1, (5120, 6144): 4, (5120, 10240): 4, (5120, 5120): 8}
     if (K, N) in want:
         assert skg == want[(K, N)]
