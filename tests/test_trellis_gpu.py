@@ -168,15 +168,16 @@ def test_two_part_split():
 
 
 @pytest.mark.parametrize("name,K,N", WL.LAYER_SHAPES)
-def test_config1_shapes_m1_m8(name, K, N):
-    """Config 1: every projection of the 27B-class layer at KB 4 and 5, M 1 and 8."""
+def test_config1_shapes_m1_to_m8(name, K, N):
+    """Config 1: every projection of the 27B-class layer at KB 4 and 5, M 1, 2, 4 and 8 (the decode step and the
+    verify batches), each against the oracle's sums."""
     for KB in (4, 5):
         banner("config1", name, K, N, KB)
         words, svh, a, _, _ = _linear_case(K, N, KB, 8, hash(name) % 1000)
         q = O.decode_pair_grid(words, K, N, KB)
         ref = O.raw_sums(a, q)
         w_d = dev(words)
-        for M in (1, 8):
+        for M in (1, 2, 4, 8):
             raw = api.trellis_gemm_m64(dev(a[:M]), w_d, None, K, N, KB, raw=True)
             torch.cuda.synchronize()
             assert close_rel(raw.cpu().numpy(), ref[:M], RAW_REL, RAW_FLOOR) <= 1.0, (KB, M)
