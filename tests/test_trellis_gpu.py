@@ -76,6 +76,7 @@ def _linear_case(K, N, KB, M, seed, skg=None, two_part=False):
     (4, 128, 128, 1, 1), (4, 512, 256, 1, 4), (4, 512, 256, 3, 2), (5, 768, 384, 8, 3),
     (3, 512, 128, 2, 1), (4, 1024, 512, 16, 8), (4, 1024, 256, 17, 4), (4, 512, 256, 64, 2),
     (5, 512, 128, 40, 1), (4, 5120, 5120, 1, None), (5, 5120, 5120, 1, None), (4, 5120, 1024, 8, None),
+    (4, 2048, 256, 3, 16), (5, 4096, 384, 9, 32),   # SKG > 8: several slices per run of the finish
 ])
 def test_gemm_raw_and_full(KB, K, N, M, skg):
     banner("gemm", KB, K, N, M, skg)
