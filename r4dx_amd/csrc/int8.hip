@@ -153,16 +153,18 @@ __global__ __launch_bounds__(256) void xq_blk_kernel(R4XSrc src, int K, int nout
   }
 }
 
-// one scale per row: a workgroup (4 waves) per row transforms every block into LDS (f16, [nout][K]), takes the
-// row's amax, then quantizes like q_row_kernel
+// one scale per row: a workgroup (kXqRowWaves waves) per row transforms every block into LDS (f16, [nout][K]),
+// takes the row's amax, then quantizes like q_row_kernel. 16 waves per row: with 4 (one per SIMD) each wave walked
+// its blocks one memory round trip at a time (K 17408: 26 us per launch)
+constexpr int kXqRowWaves = 16;
 template <int SRC>
-__global__ __launch_bounds__(256) void xq_row_kernel(R4XSrc src, int K, int nout, XqOut p, float scale) {
+__global__ __launch_bounds__(64 * kXqRowWaves) void xq_row_kernel(R4XSrc src, int K, int nout, XqOut p, float scale) {
   extern __shared__ unsigned short rowbuf[];
-  __shared__ float red[kXqMaxOut][4];
+  __shared__ float red[kXqMaxOut][kXqRowWaves];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int row = blockIdx.x, nkb = K >> 7;
   float amax[kXqMaxOut] = {0.f, 0.f, 0.f};
-  for (int kb = w; kb < nkb; kb += 4) {
+  for (int kb = w; kb < nkb; kb += kXqRowWaves) {
     const size_t k0 = (size_t)kb * 128;
     const float x0 = r4_xsrc<SRC, true>(src, row, (long long)k0 + lane);
     const float x1 = r4_xsrc<SRC, true>(src, row, (long long)k0 + lane + 64);
@@ -184,9 +186,12 @@ __global__ __launch_bounds__(256) void xq_row_kernel(R4XSrc src, int K, int nout
   }
   __syncthreads();
   for (int o = 0; o < nout; ++o) {
-    const float s = q_scale(__builtin_fmaxf(__builtin_fmaxf(red[o][0], red[o][1]), __builtin_fmaxf(red[o][2], red[o][3])));
+    float m = red[o][0];
+#pragma unroll
+    for (int i = 1; i < kXqRowWaves; ++i) m = __builtin_fmaxf(m, red[o][i]);
+    const float s = q_scale(m);
     if (threadIdx.x == 0) p.sa[o][row] = s;
-    for (int k = threadIdx.x * 4; k < K; k += 1024) {
+    for (int k = threadIdx.x * 4; k < K; k += 4 * 64 * kXqRowWaves) {
       float v[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[j] = r4_f16_to_f32(rowbuf[(size_t)o * K + k + j]);
@@ -201,11 +206,11 @@ void xq_launch(bool row_scale, const R4XSrc& src, int64_t K, int nout, const XqO
   hipStream_t st = (hipStream_t)stream;
   if (row_scale) {
     const size_t lds = (size_t)nout * K * 2;
-    // the row's values plus the kernel's 48 static bytes must fit the 160 KiB of a workgroup
+    // the row's values plus the kernel's 192 static bytes must fit the 160 KiB of a workgroup
     if (lds > 160 * 1024 - 256) r4d::fail(entry, "nout K 2 bytes must stay below 160 KiB of LDS");
     static std::atomic<unsigned long long> lds_set{0};
     if (lds > 64 * 1024) r4d::allow_lds((const void*)xq_row_kernel<SRC>, lds_set, entry);
-    hipLaunchKernelGGL((xq_row_kernel<SRC>), dim3(256), dim3(256), lds, st, src, (int)K, nout, p, scale);
+    hipLaunchKernelGGL((xq_row_kernel<SRC>), dim3(256), dim3(64 * kXqRowWaves), lds, st, src, (int)K, nout, p, scale);
   } else {
     const long long waves = 256LL * (K / 128);
     hipLaunchKernelGGL((xq_blk_kernel<SRC>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, src, (int)K, nout,
