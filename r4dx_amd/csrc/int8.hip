@@ -109,47 +109,69 @@ struct XqOut {
   float* sa[kXqMaxOut];
 };
 // the transformed block of (row, k0) for output o: lane l gets the f16 bits of elements l and l + 64
-__device__ __forceinline__ void xq_transform(float x0, float x1, const float* __restrict__ suh, size_t k0, int lane,
-                                             float scale, unsigned short& h0, unsigned short& h1) {
-  float v0 = x0 * suh[k0 + lane];
-  float v1 = x1 * suh[k0 + 64 + lane];
+// (s0, s1: suh of elements l and l + 64)
+__device__ __forceinline__ void xq_transform_s(float x0, float x1, float s0, float s1, int lane, float scale,
+                                               unsigned short& h0, unsigned short& h1) {
+  float v0 = x0 * s0;
+  float v1 = x1 * s1;
   r4_fwht128_wave(v0, v1, lane);
   h0 = r4_f16_rn(v0 * scale);
   h1 = r4_f16_rn(v1 * scale);
 }
 
-// per-(row, 128) scales: one wave per (row, block); the block goes through a wave-private LDS slot to reach
-// q_blk_kernel's lane map (lane l: k = 2 l, 2 l + 1)
+// per-(row, 128) scales: one wave per (row, kXqBlkU consecutive blocks), every load of its blocks issued before
+// the first transform (a block past the row re-reads the last one and is dropped); each block goes through a
+// wave-private LDS slot to reach q_blk_kernel's lane map (lane l: k = 2 l, 2 l + 1)
+constexpr int kXqBlkU = 4;
 template <int SRC>
 __global__ __launch_bounds__(256) void xq_blk_kernel(R4XSrc src, int K, int nout, XqOut p, float scale) {
   __shared__ unsigned short buf[4][128];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int nkb = K >> 7;
-  const long long id = (long long)blockIdx.x * 4 + w;
-  if (id >= 256LL * nkb) return;
-  const int row = (int)(id / nkb), kb = (int)(id % nkb);
-  const size_t k0 = (size_t)kb * 128;
-  const float x0 = r4_xsrc<SRC, true>(src, row, (long long)k0 + lane);
-  const float x1 = r4_xsrc<SRC, true>(src, row, (long long)k0 + lane + 64);
-  for (int o = 0; o < nout; ++o) {
-    unsigned short h0, h1;
-    xq_transform(x0, x1, p.suh[o], k0, lane, scale, h0, h1);
-    buf[w][lane] = h0;
-    buf[w][lane + 64] = h1;
-    // the wave reads what other lanes wrote: keep the read after the writes (and the next output's writes
-    // after this read) -- without the clobber the compiler hoists the read above the stores
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const unsigned raw = *(const unsigned*)&buf[w][2 * lane];
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const float v0 = r4_f16_to_f32((unsigned short)(raw & 0xFFFFu)), v1 = r4_f16_to_f32((unsigned short)(raw >> 16));
-    float amax = __builtin_fmaxf(__builtin_fabsf(v0), __builtin_fabsf(v1));
+  const int nkb = K >> 7, ngr = (nkb + kXqBlkU - 1) / kXqBlkU;
+  // workgroups are dealt to the 8 XCDs in turn: XCD x takes rows 32 x .. 32 x + 31 (two 16-row tiles of the A8
+  // layout), so the 8-byte pieces of one 256-byte A8 block are all written through one L2
+  const int xcd = blockIdx.x & 7;
+  const long long j = (long long)(blockIdx.x >> 3) * 4 + w;
+  if (j >= 32LL * ngr) return;
+  const int row = 32 * xcd + (int)(j & 31), kbase = (int)(j >> 5) * kXqBlkU;
+  float x0[kXqBlkU], x1[kXqBlkU];
+  size_t k0[kXqBlkU];
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, m, 64));
-    const float s = q_scale(amax);
-    if (lane == 0) p.sa[o][(size_t)kb * 256 + row] = s;
-    const unsigned q01 = ((unsigned)q_one(v0, s) & 0xFFu) | (((unsigned)q_one(v1, s) & 0xFFu) << 8);
-    const unsigned q23 = (unsigned)__shfl_xor((int)q01, 1, 64);
-    if ((lane & 1) == 0) q_store4(p.a8[o], true, row, (int)k0 + 2 * lane, K, q01 | (q23 << 16));
+  for (int u = 0; u < kXqBlkU; ++u) {
+    k0[u] = (size_t)min(kbase + u, nkb - 1) * 128;
+    x0[u] = r4_xsrc<SRC, true>(src, row, (long long)k0[u] + lane);
+    x1[u] = r4_xsrc<SRC, true>(src, row, (long long)k0[u] + lane + 64);
+  }
+  for (int o = 0; o < nout; ++o) {
+    float s0[kXqBlkU], s1[kXqBlkU];
+#pragma unroll
+    for (int u = 0; u < kXqBlkU; ++u) {
+      s0[u] = p.suh[o][k0[u] + lane];
+      s1[u] = p.suh[o][k0[u] + 64 + lane];
+    }
+#pragma unroll
+    for (int u = 0; u < kXqBlkU; ++u) {
+      if (kbase + u >= nkb) break;
+      unsigned short h0, h1;
+      xq_transform_s(x0[u], x1[u], s0[u], s1[u], lane, scale, h0, h1);
+      buf[w][lane] = h0;
+      buf[w][lane + 64] = h1;
+      // the wave reads what other lanes wrote: keep the read after the writes (and the next block's writes
+      // after this read) -- without the clobber the compiler hoists the read above the stores
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const unsigned raw = *(const unsigned*)&buf[w][2 * lane];
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const float v0 = r4_f16_to_f32((unsigned short)(raw & 0xFFFFu)), v1 = r4_f16_to_f32((unsigned short)(raw >> 16));
+      float amax = __builtin_fmaxf(__builtin_fabsf(v0), __builtin_fabsf(v1));
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, m, 64));
+      const float sc = q_scale(amax);
+      const int kb = kbase + u;
+      if (lane == 0) p.sa[o][(size_t)kb * 256 + row] = sc;
+      const unsigned q01 = ((unsigned)q_one(v0, sc) & 0xFFu) | (((unsigned)q_one(v1, sc) & 0xFFu) << 8);
+      const unsigned q23 = (unsigned)__shfl_xor((int)q01, 1, 64);
+      if ((lane & 1) == 0) q_store4(p.a8[o], true, row, (int)k0[u] + 2 * lane, K, q01 | (q23 << 16));
+    }
   }
 }
 
@@ -162,20 +184,43 @@ __global__ __launch_bounds__(64 * kXqRowWaves) void xq_row_kernel(R4XSrc src, in
   extern __shared__ unsigned short rowbuf[];
   __shared__ float red[kXqMaxOut][kXqRowWaves];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int row = blockIdx.x, nkb = K >> 7;
+  // XCD x (workgroups are dealt to the 8 XCDs in turn) takes rows 32 x .. 32 x + 31: the 8-byte pieces of one
+  // 256-byte A8 block (16 rows) are then all written through one L2
+  const int row = 32 * (blockIdx.x & 7) + (blockIdx.x >> 3), nkb = K >> 7;
   float amax[kXqMaxOut] = {0.f, 0.f, 0.f};
-  for (int kb = w; kb < nkb; kb += kXqRowWaves) {
-    const size_t k0 = (size_t)kb * 128;
-    const float x0 = r4_xsrc<SRC, true>(src, row, (long long)k0 + lane);
-    const float x1 = r4_xsrc<SRC, true>(src, row, (long long)k0 + lane + 64);
+  // kXqRowU blocks per pass, all their loads issued first (a block past the row re-reads the last one and is
+  // dropped), so a wave waits for one memory round trip per pass instead of one per block
+  constexpr int kXqRowU = 3;
+  for (int kb = w; kb < nkb; kb += kXqRowU * kXqRowWaves) {
+    float x0[kXqRowU], x1[kXqRowU];
+    size_t k0[kXqRowU];
+#pragma unroll
+    for (int u = 0; u < kXqRowU; ++u) {
+      const int b = min(kb + u * kXqRowWaves, nkb - 1);
+      k0[u] = (size_t)b * 128;
+      x0[u] = r4_xsrc<SRC, true>(src, row, (long long)k0[u] + lane);
+      x1[u] = r4_xsrc<SRC, true>(src, row, (long long)k0[u] + lane + 64);
+    }
 #pragma unroll
     for (int o = 0; o < kXqMaxOut; ++o) {
       if (o >= nout) break;
-      unsigned short h0, h1;
-      xq_transform(x0, x1, p.suh[o], k0, lane, scale, h0, h1);
-      rowbuf[(size_t)o * K + k0 + lane] = h0;
-      rowbuf[(size_t)o * K + k0 + lane + 64] = h1;
-      amax[o] = __builtin_fmaxf(amax[o], __builtin_fmaxf(__builtin_fabsf(r4_f16_to_f32(h0)), __builtin_fabsf(r4_f16_to_f32(h1))));
+      float s0[kXqRowU], s1[kXqRowU];
+#pragma unroll
+      for (int u = 0; u < kXqRowU; ++u) {
+        s0[u] = p.suh[o][k0[u] + lane];
+        s1[u] = p.suh[o][k0[u] + 64 + lane];
+      }
+#pragma unroll
+      for (int u = 0; u < kXqRowU; ++u) {
+        unsigned short h0, h1;
+        xq_transform_s(x0[u], x1[u], s0[u], s1[u], lane, scale, h0, h1);
+        if (kb + u * kXqRowWaves < nkb) {
+          rowbuf[(size_t)o * K + k0[u] + lane] = h0;
+          rowbuf[(size_t)o * K + k0[u] + lane + 64] = h1;
+          amax[o] = __builtin_fmaxf(amax[o], __builtin_fmaxf(__builtin_fabsf(r4_f16_to_f32(h0)),
+                                                             __builtin_fabsf(r4_f16_to_f32(h1))));
+        }
+      }
     }
   }
 #pragma unroll
@@ -212,7 +257,7 @@ void xq_launch(bool row_scale, const R4XSrc& src, int64_t K, int nout, const XqO
     if (lds > 64 * 1024) r4d::allow_lds((const void*)xq_row_kernel<SRC>, lds_set, entry);
     hipLaunchKernelGGL((xq_row_kernel<SRC>), dim3(256), dim3(64 * kXqRowWaves), lds, st, src, (int)K, nout, p, scale);
   } else {
-    const long long waves = 256LL * (K / 128);
+    const long long waves = 256LL * ((K / 128 + kXqBlkU - 1) / kXqBlkU);
     hipLaunchKernelGGL((xq_blk_kernel<SRC>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, src, (int)K, nout,
                        p, scale);
   }
