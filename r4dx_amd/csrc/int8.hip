@@ -45,15 +45,18 @@ __device__ __forceinline__ unsigned q_pack4(const float (&v)[4], float s) {
   return p;
 }
 
-// Row scales: one workgroup (256 threads) per (row, part). x f16 [M][K] (+ part * part_stride).
-__global__ __launch_bounds__(256) void q_row_kernel(const unsigned short* __restrict__ x, signed char* __restrict__ a8,
-                                                    float* __restrict__ sa, int M, int K, long long part_stride,
-                                                    int ref_layout) {
-  __shared__ float red[4];
-  const int row = blockIdx.x, part = blockIdx.y;
+// Row scales: one workgroup (kQRowWaves waves) per (row, part). x f16 [M][K] (+ part * part_stride). In the A8
+// layout (M = 256) XCD x (workgroups are dealt to the 8 XCDs in turn) takes rows 32 x .. 32 x + 31, so the 8-byte
+// pieces of one 256-byte A8 block (16 rows) are all written through one L2.
+constexpr int kQRowWaves = 16;
+__global__ __launch_bounds__(64 * kQRowWaves) void q_row_kernel(const unsigned short* __restrict__ x,
+                                                                signed char* __restrict__ a8, float* __restrict__ sa,
+                                                                int M, int K, long long part_stride, int ref_layout) {
+  __shared__ float red[kQRowWaves];
+  const int row = ref_layout ? 32 * (blockIdx.x & 7) + (blockIdx.x >> 3) : blockIdx.x, part = blockIdx.y;
   const unsigned short* xr = x + part * part_stride + (size_t)row * K;
   float amax = 0.f;
-  for (int k = threadIdx.x * 4; k < K; k += 1024) {
+  for (int k = threadIdx.x * 4; k < K; k += 4 * 64 * kQRowWaves) {
     const r4u2 raw = *(const r4u2*)(xr + k);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -63,10 +66,13 @@ __global__ __launch_bounds__(256) void q_row_kernel(const unsigned short* __rest
   for (int o = 32; o >= 1; o >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, o, 64));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
   __syncthreads();
-  const float s = q_scale(__builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3])));
+  float m = red[0];
+#pragma unroll
+  for (int i = 1; i < kQRowWaves; ++i) m = __builtin_fmaxf(m, red[i]);
+  const float s = q_scale(m);
   if (threadIdx.x == 0) sa[(size_t)part * M + row] = s;
   signed char* out = a8 + (size_t)part * M * K;
-  for (int k = threadIdx.x * 4; k < K; k += 1024) {
+  for (int k = threadIdx.x * 4; k < K; k += 4 * 64 * kQRowWaves) {
     const r4u2 raw = *(const r4u2*)(xr + k);
     float v[4];
 #pragma unroll
@@ -75,15 +81,26 @@ __global__ __launch_bounds__(256) void q_row_kernel(const unsigned short* __rest
   }
 }
 
-// Per-(row, 128) scales: one wave per (row, block); lane l takes k = 128 b + 2 l, 2 l + 1. sa [K/128][M].
+// Per-(row, 128) scales: one wave per (row, block); lane l takes k = 128 b + 2 l, 2 l + 1. sa [K/128][M]. In the
+// A8 layout (M = 256) XCD x takes rows 32 x .. 32 x + 31, as in q_row_kernel.
 __global__ __launch_bounds__(256) void q_blk_kernel(const unsigned short* __restrict__ x, signed char* __restrict__ a8,
                                                     float* __restrict__ sa, int M, int K, long long part_stride,
                                                     int ref_layout) {
   const int lane = threadIdx.x & 63;
   const int nkb = K >> 7;
-  const long long id = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (id >= (long long)M * nkb) return;
-  const int row = (int)(id / nkb), kb = (int)(id % nkb), part = blockIdx.y;
+  int row, kb;
+  if (ref_layout) {
+    const long long j = (long long)(blockIdx.x >> 3) * 4 + (threadIdx.x >> 6);
+    if (j >= 32LL * nkb) return;
+    row = 32 * (int)(blockIdx.x & 7) + (int)(j & 31);
+    kb = (int)(j >> 5);
+  } else {
+    const long long id = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (id >= (long long)M * nkb) return;
+    row = (int)(id / nkb);
+    kb = (int)(id % nkb);
+  }
+  const int part = blockIdx.y;
   const unsigned short* xr = x + part * part_stride + (size_t)row * K + kb * 128;
   const unsigned raw = *(const unsigned*)(xr + 2 * lane);
   const float v0 = r4_f16_to_f32((unsigned short)(raw & 0xFFFFu)), v1 = r4_f16_to_f32((unsigned short)(raw >> 16));
@@ -336,7 +353,7 @@ void quant_run(bool blk, int64_t x, int64_t a8, int64_t sa, int parts, int64_t p
                        (const unsigned short*)x, (signed char*)a8, (float*)sa, M, K, (long long)part_stride,
                        ref_layout ? 1 : 0);
   } else {
-    hipLaunchKernelGGL(q_row_kernel, dim3((unsigned)M, (unsigned)parts), dim3(256), 0, st, (const unsigned short*)x,
+    hipLaunchKernelGGL(q_row_kernel, dim3((unsigned)M, (unsigned)parts), dim3(64 * kQRowWaves), 0, st, (const unsigned short*)x,
                        (signed char*)a8, (float*)sa, M, K, (long long)part_stride, ref_layout ? 1 : 0);
   }
   r4d::launch_ok(entry);
