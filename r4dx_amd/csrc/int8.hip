@@ -12,10 +12,6 @@
 
 namespace {
 
-typedef __amdgpu_buffer_rsrc_t r4_rsrc;
-__device__ __forceinline__ r4_rsrc mk_rsrc(const void* p, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
-}
 
 // ---- the A8 fragment layout (r4d_trellis_i8_layout.h:32-45) -----------------------------------------
 __host__ __device__ inline size_t a8_offset(int r, int k, int K) {
