@@ -12,7 +12,6 @@
 
 namespace {
 
-
 // ---- the A8 fragment layout (r4d_trellis_i8_layout.h:32-45) -----------------------------------------
 __host__ __device__ inline size_t a8_offset(int r, int k, int K) {
   const int k16 = k & 15, h = (k16 >> 2) & 1, e = 4 * (k16 >> 3) + (k16 & 3);
