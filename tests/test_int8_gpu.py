@@ -30,9 +30,9 @@ def _oracle_quant(x, blk):
 
 @pytest.mark.parametrize("blk", [False, True])
 @pytest.mark.parametrize("ref_layout", [False, True])
-def test_quantizers_bit_exact(blk, ref_layout):
-    banner("i8 quant", blk, ref_layout)
-    K = 5120
+@pytest.mark.parametrize("K", [5120, 1152, 17408])   # 1152: a row shorter than one pass of the row kernel
+def test_quantizers_bit_exact(blk, ref_layout, K):
+    banner("i8 quant", blk, ref_layout, K)
     x, _, _ = WL.int8_case(K, 128, 1)
     x[3, :] = 0                      # an all-zero row: scale 1
     x[5, 256:384] = 0                # an all-zero block
@@ -162,7 +162,8 @@ def test_config4(K, N):
 
 
 @pytest.mark.parametrize("row_scale", [False, True])
-@pytest.mark.parametrize("K,nout,prescale", [(5120, 1, 0), (17408, 1, 3), (1024, 2, -4), (2048, 3, 0)])
+@pytest.mark.parametrize("K,nout,prescale", [(5120, 1, 0), (17408, 1, 3), (1024, 2, -4), (2048, 3, 0),
+                                              (1152, 2, 1)])   # 9 blocks: a partial group of the per-128 form
 def test_fused_transform_quantizer_bit_exact(row_scale, K, nout, prescale):
     """r4dx_trellis_input_i8(r) == r4dx_trellis_input_bf16 then r4d_trellis_i8_quant_act(_row), byte for byte."""
     banner("xq", row_scale, K, nout, prescale)
