@@ -83,7 +83,7 @@ def main():
     lin, groups = [], []
     for gi, (gname, members) in enumerate(WL.LAYER_GROUPS):
         K = shape[members[0][0]][0]
-        x = torch.from_numpy(WL.activations_f16(M, K, 30 + gi)).to(dev)
+        x = torch.from_numpy(WL.activations_f16(M, K, 30 + gi, bf16_exact=True)).to(dev)
         g = dict(name=gname, x=x, suh=[], outs=[])
         for li, parts in enumerate(members):
             N = sum(shape[p][1] for p in parts)
@@ -372,7 +372,7 @@ def config1_layer(api, WL, M, kb_of, gen, min_bytes=1 << 30):
         parts = len(widths)
         layer.append(dict(
             name=gname, K=K, N=N, KB=KB, skg=skg, n0=[int(v) for v in np.cumsum([0] + widths[:-1])],
-            x=torch.from_numpy(WL.activations_f16(M, K, 30 + gi)).to(dev),
+            x=torch.from_numpy(WL.activations_f16(M, K, 30 + gi, bf16_exact=True)).to(dev),
             suh=[torch.from_numpy(WL.signs(K, 10 + 3 * gi + j)).to(dev) for j in range(parts)],
             a=[torch.empty((M, K), dtype=torch.float16, device=dev) for _ in range(parts)],
             words=[torch.randint(-2**31, 2**31 - 1, (nw,), dtype=torch.int32, device=dev, generator=gen)
@@ -882,54 +882,59 @@ def bench_trellis_i8(api, WL, KB, R=4):
 
 
 def cpu_baseline(KB):
-    """The CPU oracle's decode + fp64 linear of config 0 (K = N = 5120, M = 1) on all host cores."""
+    """The reference's own CPU path for config 0 (K = N = 5120, M = 1): input transform, pair-grid decode, fp64 linear
+    (trellis_ref.hpp compiled into oracle/_ref, single-threaded as written), beside the oracle's port of the same work
+    on all host cores; each the median of at least 5 runs. x is the GPU leg's kind of input: f16 ~N(0,1) with values
+    exact in bf16, because the reference's CPU TransformInput reads bf16 x (trellis_ref.hpp:150) -- both forms then
+    read the same numbers."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     from r4dx_amd import workloads as WL
     K = N = 5120
     words, suh, svh = WL.trellis_linear(K, N, KB, 1)
-    x = WL.activations_f16(1, K, 2).view(np.uint16)
+    x = WL.activations_f16(1, K, 2, bf16_exact=True).view(np.uint16)
     lib = O.lib()
     cores = lib.r4o_max_threads()
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
+
+    def med(fn, budget_s, nmax):
+        ts = []
+        t_all = time.perf_counter()
+        while len(ts) < 5 or (time.perf_counter() - t_all < budget_s and len(ts) < nmax):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)), len(ts)
+
+    def port_run():
         a = O.transform_input(x, False, suh, 0)
         q = O.decode_pair_grid(words, K, N, KB, 0)
         O.linear_from_a(a, q, svh, 0, nthreads=0)
-        reps += 1
-        if time.perf_counter() - t0 > 10.0 or reps >= 20:
-            break
-    dt = (time.perf_counter() - t0) / reps
+    dt, n = med(port_run, 5.0, 20)
     port = {"value": round(K * N * KB / 8 / dt / 1e9, 4), "unit": "GB/s", "cores": cores,
-            "kind": "port", "sample": f"config0 K=N=5120 KB={KB} M=1: transform + decode + fp64 linear, "
-                                      f"{reps} runs, {dt * 1e3:.1f} ms each"}
+            "kind": "port", "sample": f"config0 K=N=5120 KB={KB} M=1 (f16 x, values exact in bf16): transform + "
+                                      f"decode + fp64 linear, median of {n} runs, {dt * 1e3:.1f} ms"}
     ref = O.ref()
     if ref is None:
         return port
-    # the reference's own CPU path (tests/kernels/trellis_ref.hpp compiled into oracle/_ref), single-threaded as
-    # it is written: input transform, pair-grid decode, fp64 linear
     from oracle_lib import ptr
     xb = O.f32_to_bf16_bits(O.f16_bits_to_f32(x))
+    assert np.array_equal(O.bf16_bits_to_f32(xb), O.f16_bits_to_f32(x)), "x must be exact in bf16"
     a = np.empty((1, K), np.uint16)
     q = np.empty((K, N), np.uint16)
     y = np.empty((1, N), np.float64)
     svh32 = np.ascontiguousarray(svh, np.float32)
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        ref.ref_transform_input_bf16(ptr(xb), 1, K, ptr(np.ascontiguousarray(suh, np.float32)), 0, ptr(a))
+    suh32 = np.ascontiguousarray(suh, np.float32)
+
+    def ref_run():
+        ref.ref_transform_input_bf16(ptr(xb), 1, K, ptr(suh32), 0, ptr(a))
         ref.ref_decode_pair_grid(ptr(words), K, N, KB, ptr(q))
         ref.ref_linear_from_a(ptr(a), None, N, 1, K, N, ptr(q), ptr(svh32), 0, ptr(y))
-        reps += 1
-        if time.perf_counter() - t0 > 15.0 or reps >= 10:
-            break
-    dt = (time.perf_counter() - t0) / reps
+    dt, n = med(ref_run, 10.0, 10)
     return {"value": round(K * N * KB / 8 / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "reference",
-            "sample": f"config0 K=N=5120 KB={KB} M=1 (bf16 x): the reference's trellis_ref.hpp transform + "
-                      f"pair-grid decode + fp64 linear, single-threaded as written, {reps} runs, {dt * 1e3:.1f} ms "
-                      f"each", "port_all_cores": port}
+            "sample": f"config0 K=N=5120 KB={KB} M=1 (the same x as bf16): the reference's trellis_ref.hpp transform + "
+                      f"pair-grid decode + fp64 linear, single-threaded as written, median of {n} runs, "
+                      f"{dt * 1e3:.1f} ms", "port_all_cores": port}
 
 
 def cpu_baselines_other(KB):

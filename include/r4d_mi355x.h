@@ -76,8 +76,9 @@ void r4dx_trellis_gemv_xf_parts(int64_t x, int x_is_bf16, const int64_t* suh, co
  * serving loops that forbid hipMalloc). r4d_gemm_trellis_nt_m64 (same C, A parts, SK and SKG meaning) with no ws or
  * tickets argument: the split partials and tickets live in a device array the library holds per GPU until the
  * process ends (16 MiB of partials -- SKG M N 4 bytes at most, r4dx_gemm_trellis_nt_m64_noalloc_max_ws_bytes() --
- * and tickets for N up to 262144). Nothing is allocated on any call. Every call on one GPU shares that GPU's array:
- * calls that overlap on one GPU race. The _check form returns NULL or the rule a launch breaks (sizes beyond the
+ * and tickets for N up to 262144). Nothing is allocated on any call. Every call on one GPU shares that GPU's array,
+ * whatever its stream: calls that overlap on one GPU race, so callers on several streams of one GPU (an MTP head
+ * beside the model) must order their calls (one stream, or events between them). The _check form returns NULL or the rule a launch breaks (sizes beyond the
  * array included); the entry throws on the same. */
 void r4dx_gemm_trellis_nt_m64_noalloc(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c, int M,
                                       int K, int N, int KB, int SK, int SKG, float out_scale, int64_t stream);
@@ -110,8 +111,8 @@ int r4d_mi355x_trellis_m256_skg(int K, int N, int KB);
 /* ---- w4a16 group-quantized skinny GEMM (LM head, drafters) ------------------------------------- */
 /* r4d.h:331-333: C bf16 [M][N] = A f16 [M][K] @ dequant(Wq, Wsz)^T at the build-default group 64; Wq in
  * the packed fragment order of quant_int4.hpp:171-198, Wsz (tile, group, row) dwords = f16 scale | f16
- * (-(1024 + zero)) << 16. WV, SK, MB, NPW, NT accepted and unused. M 1..64 (M x K bounded by the LDS
- * copy of A: M <= 8 at K = 5120), N % 16 == 0, K % 64 == 0. */
+ * (-(1024 + zero)) << 16. WV, SK, MB, NPW, NT accepted and unused. M 1..64 at any K (A is staged in LDS in
+ * K chunks), N % 16 == 0, K % 64 == 0. */
 void r4d_gemm_w4a16_nt_m64(int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int N, int WV, int SK,
                            int MB, int NPW, int NT, int64_t stream);
 int  r4d_gemm_w4a16_nt_m64_max_m(void);            /* r4d.h:333 */

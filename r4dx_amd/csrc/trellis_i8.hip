@@ -582,6 +582,9 @@ std::string ti8_check(int M, int K, int N, int n_split, int KB, int skw, int skg
   if (skg != 1 && skg != 2 && skg != 4 && skg != 8) return "skg must be 1, 2, 4 or 8";
   if ((K / 128) % (skw * skg)) return "(K / 128) must be divisible by skw * skg";
   if ((long long)256 * K >= (1LL << 32)) return "256 K must be below 2^32 bytes";
+  // a split launch's fp32 slices go through the prefill GEMM's finish, which addresses them with 32-bit offsets
+  if (skg > 1 && (long long)skg * 256 * N * 4 > (1LL << 31))
+    return "the fp32 slices skg * 256 * N * 4 bytes must fit 2 GiB (32-bit offsets of the split finish): lower skg";
   return "";
 }
 

@@ -58,6 +58,9 @@ __device__ __forceinline__ int m2_bslot(int n, int c) { return c * 2048 + ((n ^ 
 // wait cannot deadlock; it is bounded anyway, and a wait that runs out poisons its results with NaN.
 constexpr int kSegWhole = 0, kSegPublish = 1, kSegContinue = 2;
 constexpr int kFlagStride = 4;            // words between two workgroups' flags
+// Workgroup c's flag is word kFlagStride c + 1 of the ticket buffer: never word 32 g, the counter of 128-column group g
+// that the M <= 64 kernel's split hand-over takes tickets on, so a flag left set can never be read as a ticket count.
+__device__ __forceinline__ unsigned* m2_flag(unsigned* flags, unsigned c) { return flags + (size_t)c * kFlagStride + 1; }
 
 // A workgroup's share: steps [beg, end) of the launch's units in order (unit u = group * SKG + y, nst steps each).
 struct M2Share {
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
     bool poisoned = false;                                                                                 \
     if (kind == kSegContinue) {                                                                            \
       if (threadIdx.x == 0) {                                                                              \
-        unsigned* f = flags + (size_t)(blockIdx.x - 1) * kFlagStride;                                      \
+        unsigned* f = m2_flag(flags, blockIdx.x - 1);                                                        \
         int spin = 0;                                                                                      \
         while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u && spin < (1 << 24)) { \
           __builtin_amdgcn_s_sleep(8);                                                                     \
@@ -334,7 +337,7 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       __syncthreads();
       if (threadIdx.x == 0)
-        __hip_atomic_store(flags + (size_t)blockIdx.x * kFlagStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(m2_flag(flags, blockIdx.x), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       continue;
     }
 
@@ -521,6 +524,9 @@ std::string m256_check(int M, int K, int N, int n_split, int KB, int SKG) {
   if (KB != 3 && KB != 4 && KB != 5) return "KB " + str(KB) + " is not instantiated (3, 4, 5)";
   if (SKG < 1 || SKG > 64 || (K / 16) % (4 * SKG)) return "SKG must be 1..64 with (K/16) divisible by 4 SKG";
   if (n_split < 0 || n_split > N || n_split % 128) return "n_split must be in 0..N and a multiple of 128";
+  // the kernel's stores and the split finish address one slice, and all SKG slices, with 32-bit buffer offsets
+  if ((long long)SKG * M * N * 4 > (1LL << 31))
+    return "the fp32 slices SKG * M * N * 4 bytes must fit 2 GiB (32-bit offsets of the split finish): lower SKG";
   return "";
 }
 
@@ -541,7 +547,7 @@ int m256_balanced_p(int M, int N, int SKG, bool have_ws, bool have_tickets) {
   (void)M;
   const int G = N / 128, U = G * SKG, cus = m256_cus();
   if (!have_ws || !have_tickets || U <= cus || U % cus == 0) return 0;
-  if ((long long)cus * kFlagStride > (long long)G * R4_TICKET_WORDS) return 0;   // the flags fit the ticket buffer
+  if ((long long)cus * kFlagStride + 1 > (long long)G * R4_TICKET_WORDS) return 0;   // the flags fit the ticket buffer
   return cus;
 }
 

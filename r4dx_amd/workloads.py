@@ -63,12 +63,18 @@ def svh_scales(N, seed):
     return s.astype(np.float16).astype(np.float32)
 
 
-def activations_f16(M, K, seed, outlier_frac=0.0, outlier_scale=20.0):
+def activations_f16(M, K, seed, outlier_frac=0.0, outlier_scale=20.0, bf16_exact=False):
+    """f16 activations ~N(0,1) (a fraction of columns scaled as outlier channels). bf16_exact: each value rounded
+    first to bf16 precision (nearest even), so the same numbers are exact in bf16 and in f16 (|x| < 2^16) -- an input
+    that the bf16 and the f16 forms of the input transform read identically."""
     rng = np.random.default_rng(seed)
     x = rng.standard_normal((M, K)).astype(np.float32)
     if outlier_frac > 0:
         cols = rng.choice(K, max(1, int(round(K * outlier_frac))), replace=False)
         x[:, cols] *= outlier_scale
+    if bf16_exact:
+        u = x.view(np.uint32).astype(np.uint64)
+        x = (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
     return x.astype(np.float16)
 
 

@@ -100,6 +100,19 @@ def test_m256_checks(L):
     for K, N in [(5120, 17408), (17408, 5120), (5120, 1024), (6144, 5120)]:
         skg = L.r4d_mi355x_trellis_m256_skg(K, N, 4)
         assert ck(256, K, N, N, 4, 0, 0, skg, 0, 0) is None
+    # the kernel's stores and the split finish address the fp32 slices with 32-bit offsets: SKG M N 4 must fit 2 GiB
+    assert ck(256, 2048, 262144, 262144, 4, 0, 0, 8, 0, 0) is None
+    assert b"2 GiB" in ck(256, 2048, 262144 + 128, 262144 + 128, 4, 0, 0, 8, 0, 0)
+    assert ck(128, 2048, 262144 + 128, 262144 + 128, 4, 0, 0, 8, 0, 0) is None
+
+
+def test_trellis_i8_check_bounds_the_split_slices(L):
+    """A split trellis-int8 launch sums its fp32 slices in the prefill GEMM's finish (32-bit offsets): skg 256 N 4
+    bytes must fit 2 GiB; unsplit launches write no slices."""
+    ck = L.r4d_gemm_trellis_nt_i8_check
+    assert ck(256, 2048, 262144, 262144, 4, 2, 8) is None
+    assert b"2 GiB" in ck(256, 2048, 262144 + 128, 262144 + 128, 4, 2, 8)
+    assert ck(256, 2048, 262144 + 128, 262144 + 128, 4, 2, 1) is None
 
 
 def test_w4a16_checks(L):

@@ -36,7 +36,9 @@ def _noalloc(f, ck, a, w, svh, K, N, KB, SK, SKG, out):
 
 def test_noalloc_equals_caller_buffer_entry_two_calls():
     L, f, ck = _entry()
-    cases = [(5120, 17408, 4, 8, 0, None), (5120, 6144, 5, 1, 0, None), (6144, 5120, 4, 4, 1, 4)]
+    # the last case fills the array: 8 slices x 64 rows x 8192 columns x 4 bytes = 16 MiB of partials
+    cases = [(5120, 17408, 4, 8, 0, None), (5120, 6144, 5, 1, 0, None), (6144, 5120, 4, 4, 1, 4),
+             (5120, 8192, 4, 64, 0, 8)]
     for K, N, KB, M, SK, skg in cases:
         banner("noalloc", K, N, KB, M, SK, skg)
         skg = api.trellis_gemv_skg(K, N, KB) if skg is None else skg
@@ -63,5 +65,7 @@ def test_noalloc_size_rule():
     cap = L.r4dx_gemm_trellis_nt_m64_noalloc_max_ws_bytes()
     assert cap == 16 << 20
     assert ck(8, 5120, 34816, 34816, 4, 2) is None                      # 2.2 MB of partials
+    assert ck(64, 5120, 8192, 8192, 4, 8) is None                       # exactly 16 MiB
+    assert b"exceed the scratch" in ck(64, 5120, 8192 + 128, 8192 + 128, 4, 8)
     assert b"exceed the scratch" in ck(64, 5120, 34816, 34816, 4, 8)    # 71 MB
     assert b"N must be at most" in ck(1, 5120, 262144 + 128, 262144 + 128, 4, 1)
