@@ -195,7 +195,10 @@ void   r4d_trellis_i8_wscale(int64_t w, int64_t sw, int K, int N, int KB, int64_
 void   r4d_trellis_i8_dump_w(int64_t w, int64_t sw, int64_t w8, int64_t wp, int K, int N, int KB, int64_t stream);
 /* r4d.h:495-499: C bf16 [256][N] = bf16((FWHT128(sum_kb float(int32(A8 . W8)) * (sa sw)) * svh) * out_scale);
  * columns >= n_split read a8_1 / sa_1 (a8_1 = 0: a8_0, then n_split = N); ws fp32 ws_bytes(M, N, skg) when
- * skg > 1 (then a second launch adds the slices); tickets accepted and unused; skw checked, not used. */
+ * skg > 1 (then a second launch adds the slices); tickets accepted and unused; skw checked, not used.
+ * SW must be a table of r4d_trellis_i8_wscale (each entry the correctly rounded fp32 1 / rs of an f16 rs): the
+ * kernel recovers rs from it with the hardware reciprocal, which returns that rs exactly for such entries only (an
+ * arbitrary fp32 scale can round to a different rs than the reference's divide). */
 void r4d_gemm_trellis_nt_i8(int64_t a8_0, int64_t sa_0, int64_t a8_1, int64_t sa_1, int n_split, int64_t w,
                             int64_t sw, int64_t svh, int64_t c, int64_t ws, int64_t tickets, int M, int K, int N,
                             int KB, int skw, int skg, float out_scale, int64_t stream);

@@ -172,3 +172,25 @@ def test_m256_balanced_repeats_and_resets_flags():
         torch.cuda.synchronize()
         assert torch.equal(again.view(torch.int16), first.view(torch.int16))
         assert int(tk.abs().sum().item()) == 0
+
+
+def test_balanced_flags_leave_the_ticket_words_clear():
+    """The balanced form's hand-over flags share the linear's ticket buffer with the M <= 64 split: after a balanced
+    launch every word of the buffer is back at zero, and a split GEMV launch on the same buffer gives the bits of one
+    on a fresh buffer (a flag never lands on a group's counter word)."""
+    banner("m256 flags / tickets")
+    K, N, KB = 1024, 33024, 5                     # 258 column groups: more than the CUs, not a multiple
+    words, _, svh = WL.trellis_linear(K, N, KB, 77)
+    a = WL.activations_f16(256, K, 78).view(np.uint16)
+    w_d, a_d, s_d = dev(words), dev(a), dev(svh)
+    tickets = api.TicketBuffer(N, w_d.device).t
+    for _ in range(3):
+        api.trellis_gemm_m256(a_d, w_d, s_d, K, N, KB, skg=1, tickets=tickets, out_scale=0.25)
+    torch.cuda.synchronize()
+    assert int(tickets.view(torch.int32).abs().sum().item()) == 0
+    a1 = a_d[:8].contiguous()
+    shared = api.trellis_gemm_m64(a1, w_d, s_d, K, N, KB, skg=4, tickets=tickets, out_scale=0.25)
+    fresh = api.trellis_gemm_m64(a1, w_d, s_d, K, N, KB, skg=4, out_scale=0.25)
+    torch.cuda.synchronize()
+    assert torch.equal(shared.view(torch.int16), fresh.view(torch.int16))
+    assert int(tickets.view(torch.int32).abs().sum().item()) == 0
