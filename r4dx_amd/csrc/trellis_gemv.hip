@@ -658,16 +658,20 @@ constexpr size_t kXfAldsMax = 96 * 1024;   // the fused transform stages the sli
 struct GemvForm {
   int NPW, SK, MT;
 };
-GemvForm gemv_form(int M, int SKG, bool have_ws, bool sk1) {
+// xf (the fused input transform): at M = 1 a workgroup of a launch with N >= 8192 holds two pairs, which halves the
+// transform work repeated per pair (every workgroup transforms its whole K slice). Measured per launch at M = 1
+// (µs, one pair / two pairs per workgroup): 5120x8192 12.0 / 11.5, 5120x16384 18.8 / 17.4, 5120x34816 34.1 / 33.2,
+// but 6144x5120 10.9 / 11.8 and 17408x5120 19.5 / 20.8 (fewer workgroups on the 160 pairs of N = 5120).
+GemvForm gemv_form(int M, int N, int SKG, bool have_ws, bool sk1, bool xf = false) {
   GemvForm f;
   f.MT = M <= 16 ? 1 : M <= 32 ? 2 : 4;
   if (sk1 || (SKG == 1 && !have_ws)) { f.NPW = 4; f.SK = 1; }
-  else { f.NPW = M == 1 ? 1 : 2; f.SK = 4; }
+  else { f.NPW = M == 1 && !(xf && N >= 8192) ? 1 : 2; f.SK = 4; }
   return f;
 }
 // The LDS bytes of a launch of that form (alds: A staged in LDS, forced by the fused transform).
-size_t gemv_form_lds(int M, int K, int SKG, bool have_ws, bool sk1, bool xf) {
-  const GemvForm f = gemv_form(M, SKG, have_ws, sk1);
+size_t gemv_form_lds(int M, int K, int N, int SKG, bool have_ws, bool sk1, bool xf) {
+  const GemvForm f = gemv_form(M, N, SKG, have_ws, sk1, xf);
   const int ktw = K / 16 / SKG;
   const bool alds = xf || gemv_ktl_pad(f.SK, ktw) * M * 32 <= kAldsMax;
   return gemv_lds(f.MT, f.NPW, f.SK, alds, ktw, M);
@@ -724,7 +728,7 @@ void launch_gemv_a(const r4d_gemv_args& a) {
 // and fewer workgroups take fewer tickets on the group's counter).
 template <int KB, int MT>
 void launch_gemv_np(const r4d_gemv_args& a) {
-  const GemvForm f = gemv_form(a.M, a.SKG, a.ws != 0 && a.tickets != 0, a.sk1 != 0);
+  const GemvForm f = gemv_form(a.M, a.N, a.SKG, a.ws != 0 && a.tickets != 0, a.sk1 != 0, a.xf != 0);
   if (f.SK == 1) launch_gemv_a<KB, MT, 4, 1>(a);
   else if (f.NPW == 1) launch_gemv_a<KB, MT, 1, 4>(a);
   else launch_gemv_a<KB, MT, 2, 4>(a);
@@ -732,7 +736,7 @@ void launch_gemv_np(const r4d_gemv_args& a) {
 
 template <int KB>
 void launch_gemv_kb(const r4d_gemv_args& a) {
-  const int mt = gemv_form(a.M, a.SKG, true, false).MT;
+  const int mt = gemv_form(a.M, a.N, a.SKG, true, false).MT;
   if (mt <= 1) launch_gemv_np<KB, 1>(a);
   else if (mt <= 2) launch_gemv_np<KB, 2>(a);
   else launch_gemv_np<KB, 4>(a);
@@ -872,9 +876,9 @@ const char* r4dx_trellis_gemv_xf_check(int M, int K, int N, int n_split, int KB,
   std::string e;
   if ((K / 128) % SKG) e = "the fused transform needs whole 128-blocks per slice: (K / 128) % SKG == 0";
   else {
-    const GemvForm f = gemv_form(M, SKG, have_ws != 0, false);
+    const GemvForm f = gemv_form(M, N, SKG, have_ws != 0, false, true);
     if (gemv_ktl_pad(f.SK, K / 16 / SKG) * M * 32 > kXfAldsMax) e = "the A slice does not fit LDS: raise SKG";
-    else if (gemv_form_lds(M, K, SKG, have_ws != 0, false, true) > 160 * 1024)
+    else if (gemv_form_lds(M, K, N, SKG, have_ws != 0, false, true) > 160 * 1024)
       e = "the A slice, the split partials and the finish buffers exceed 160 KiB of LDS: lower M or raise SKG";
   }
   return r4d::check_result(e);

@@ -47,9 +47,10 @@ def test_xf_check_bounds_the_whole_lds():
     L = loader.lib()
     ck = L.r4dx_trellis_gemv_xf_check
 
-    def lds(M, K, SKG, ws):
+    def lds(M, K, N, SKG, ws):
         split = ws or SKG > 1
-        npw, sk = (1 if M == 1 else 2, 4) if split else (4, 1)
+        # at M = 1 a fused launch with N >= 8192 holds two pairs per workgroup
+        npw, sk = (1 if M == 1 and N < 8192 else 2, 4) if split else (4, 1)
         mt = 1 if M <= 16 else 2 if M <= 32 else 4
         ktw = K // 16 // SKG
         steps = (ktw + 3) // 4
@@ -63,10 +64,11 @@ def test_xf_check_bounds_the_whole_lds():
                 continue
             for M in range(1, 65):
                 for ws in (0, 1):
-                    total, a_bytes = lds(M, K, SKG, ws)
-                    ok = ck(M, K, 1024, 1024, 4, SKG, ws) is None
-                    want = (ws or SKG == 1) and a_bytes <= 96 * 1024 and total <= 160 * 1024
-                    assert ok == want, (K, SKG, M, ws)
+                    for N in (1024, 8192):
+                        total, a_bytes = lds(M, K, N, SKG, ws)
+                        ok = ck(M, K, N, N, 4, SKG, ws) is None
+                        want = (ws or SKG == 1) and a_bytes <= 96 * 1024 and total <= 160 * 1024
+                        assert ok == want, (K, N, SKG, M, ws)
 
 
 def test_sizes_and_rates(L):
