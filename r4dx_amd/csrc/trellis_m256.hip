@@ -717,11 +717,12 @@ int r4d_mi355x_trellis_m256_skg(int K, int N, int KB) {
     // of rounds when the units are a multiple of the compute units)
     const bool balanced = units > cus && units % cus != 0;
     const double path = balanced ? (double)((units * steps + cus - 1) / cus) : (double)((units + cus - 1) / cus) * steps;
-    // measured on config 2's shapes (M = 256, one workgroup per CU): a step ~1.05 us in the data-parallel form and
-    // ~1.52 us per step of a share in the balanced form (gate | up, 272 units: 132 us balanced at SKG 1 against
-    // 155 us in three rounds at SKG 2); a split costs ~2 us (the finish launch) plus ~0.06 us per workgroup-slice
-    // (its partials written and read back)
-    const double cost = path * (balanced ? 1.52 : 1.05) + (d > 1 ? 2.0 + 0.06 * G * d : 0.0);
+    // fitted to SKG sweeps of the layer's M = 256 launch shapes (TP 1 and 2; one workgroup per CU): a step ~1.05 us
+    // in the data-parallel form and ~1.3 us per step of a share in the balanced form (measured 1.0-1.5 across
+    // shapes; 1.3 reproduces every sweep's best SKG, e.g. 17408 x 5120: SKG 4 80.4 us, SKG 8 balanced 67.6 us;
+    // 6144 x 5120: 37.9 / 43.9 us; 5120 x 34816: SKG 1 balanced 125 us, SKG 2 152 us); a split costs ~2 us (the
+    // finish launch) plus ~0.06 us per workgroup-slice (its partials written and read back)
+    const double cost = path * (balanced ? 1.3 : 1.05) + (d > 1 ? 2.0 + 0.06 * G * d : 0.0);
     if (cost < best_cost) {
       best_cost = cost;
       best = d;
