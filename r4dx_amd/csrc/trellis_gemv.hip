@@ -50,9 +50,15 @@ constexpr int kWeightPolicy = 2;
 // One step's words of this lane from the slice buffer at step byte offset so (out of range -> 0).
 template <int KB, bool HIST = true>
 __device__ __forceinline__ void load_words(Words<KB>& s, r4_rsrc r, const LaneWords<KB>& lw, unsigned so) {
-  if constexpr (KB == 4) {
+  // one wide load per lane where the KB words allow it (buffer loads need dword alignment only): KB 4 one dwordx4,
+  // KB 5 a dwordx4 and a dword, KB 3 a dwordx3 -- not KB dword loads, each of which would touch every line of the step
+  if constexpr (KB == 4 || KB == 5) {
     const r4u4 v = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(r, lw.own + so, 0, kWeightPolicy));
     s.w[1] = v[0]; s.w[2] = v[1]; s.w[3] = v[2]; s.w[4] = v[3];
+    if constexpr (KB == 5) s.w[5] = __builtin_amdgcn_raw_buffer_load_b32(r, lw.own + so + 16, 0, kWeightPolicy);
+  } else if constexpr (KB == 3) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, lw.own + so, 0, kWeightPolicy);
+    s.w[1] = v[0]; s.w[2] = v[1]; s.w[3] = v[2];
   } else {
 #pragma unroll
     for (int i = 0; i < KB; ++i) s.w[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(r, lw.own + so + 4 * i, 0, kWeightPolicy);

@@ -87,9 +87,11 @@ struct TileWords {
   }
   __device__ __forceinline__ void load(unsigned (&w)[KB + 1], int st) const {
     const unsigned so = (unsigned)st * (4u * 16u * KB * 4u);
-    if constexpr (KB == 4) {
+    // one wide load per lane (dword alignment suffices): KB 4 a dwordx4, KB 5 a dwordx4 and a dword
+    if constexpr (KB == 4 || KB == 5) {
       const r4u4 v = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(r, own + so, 0, 0));
       w[1] = v[0]; w[2] = v[1]; w[3] = v[2]; w[4] = v[3];
+      if constexpr (KB == 5) w[5] = __builtin_amdgcn_raw_buffer_load_b32(r, own + so + 16, 0, 0);
     } else {
 #pragma unroll
       for (int i = 0; i < KB; ++i) w[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(r, own + so + 4 * i, 0, 0);

@@ -174,12 +174,14 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
       auto load = [&](St& s, int st) {
         const int sc = min(st, ns - 1);
         const unsigned so = (unsigned)sc * kStepBytes;
-        if constexpr (KB == 4) {
+        // one wide load per lane (dword alignment suffices): KB 4 a dwordx4, KB 5 a dwordx4 and a dword, KB 3 a dwordx3
+        if constexpr (KB == 4 || KB == 5) {
           const r4u4 v = __builtin_bit_cast(r4u4, __builtin_amdgcn_raw_buffer_load_b128(wr, own + so, 0, 0));
           s.w[1] = v[0]; s.w[2] = v[1]; s.w[3] = v[2]; s.w[4] = v[3];
+          if constexpr (KB == 5) s.w[5] = __builtin_amdgcn_raw_buffer_load_b32(wr, own + so + 16, 0, 0);
         } else {
-#pragma unroll
-          for (int i = 0; i < KB; ++i) s.w[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(wr, own + so + 4 * i, 0, 0);
+          const auto v = __builtin_amdgcn_raw_buffer_load_b96(wr, own + so, 0, 0);
+          s.w[1] = v[0]; s.w[2] = v[1]; s.w[3] = v[2];
         }
         s.w[0] = __builtin_amdgcn_raw_buffer_load_b32(wr, hist + so, 0, 0);
 #pragma unroll
@@ -717,12 +719,13 @@ int r4d_mi355x_trellis_m256_skg(int K, int N, int KB) {
     // of rounds when the units are a multiple of the compute units)
     const bool balanced = units > cus && units % cus != 0;
     const double path = balanced ? (double)((units * steps + cus - 1) / cus) : (double)((units + cus - 1) / cus) * steps;
-    // fitted to SKG sweeps of the layer's M = 256 launch shapes (TP 1 and 2; one workgroup per CU): a step ~1.05 us
-    // in the data-parallel form and ~1.3 us per step of a share in the balanced form (measured 1.0-1.5 across
-    // shapes; 1.3 reproduces every sweep's best SKG, e.g. 17408 x 5120: SKG 4 80.4 us, SKG 8 balanced 67.6 us;
-    // 6144 x 5120: 37.9 / 43.9 us; 5120 x 34816: SKG 1 balanced 125 us, SKG 2 152 us); a split costs ~2 us (the
-    // finish launch) plus ~0.06 us per workgroup-slice (its partials written and read back)
-    const double cost = path * (balanced ? 1.3 : 1.05) + (d > 1 ? 2.0 + 0.06 * G * d : 0.0);
+    // fitted to SKG sweeps of the layer's M = 256 launch shapes (TP 1 and 2; one workgroup per CU; weights streamed
+    // from HBM, > 1 GB of copies): a step ~1.05 us in the data-parallel form and ~1.4 us per step of a share in the
+    // balanced form (all CUs busy; 1.4 reproduces every sweep's best SKG, e.g. 17408 x 5120: SKG 4 82.1 us, SKG 8
+    // balanced 80.5 us; 6144 x 5120: 37.6 / 44.0 us; 8704 x 5120: 47.3 / 53.3 us; 5120 x 34816: SKG 1 balanced
+    // 132 us, SKG 2 145 us); a split costs ~2 us (the finish launch) plus ~0.06 us per workgroup-slice (its partials
+    // written and read back)
+    const double cost = path * (balanced ? 1.4 : 1.05) + (d > 1 ? 2.0 + 0.06 * G * d : 0.0);
     if (cost < best_cost) {
       best_cost = cost;
       best = d;
