@@ -549,58 +549,73 @@ def bench_m256(api, WL, KB, R=3):
 
     # The layer as 6 launches: the projections that share an input as one linear (gdn qkv | z, attn q | k | v
     # through r4dx_gemm_trellis_nt_m256_parts; mlp gate | up through the two-part r4d_gemm_trellis_nt_m256).
+    # kb_of(group name) gives each group's rate: KB 4 throughout for the headline, then the rows at KB 5 and at
+    # config 1's 4/5 mix.
     shape = {name: (K, N) for name, K, N in WL.LAYER_SHAPES}
-    per_launch, tot_flop, tot_ms = {}, 0.0, 0.0
-    for i, (gname, members) in enumerate(WL.LAYER_GROUPS):
-        names = [p for m in members for p in m]
-        K = shape[names[0]][0]
-        widths = [shape[p][1] for p in names]
-        N = sum(widths)
-        n0 = [int(v) for v in np.cumsum([0] + widths[:-1])]
-        nw = K * N * KB // 32
-        copies = max(2, int(np.ceil(1.0e9 / (nw * 4))))
-        words = [torch.randint(-2**31, 2**31 - 1, (nw,), dtype=torch.int32, device=dev) for _ in range(copies)]
-        a = [torch.from_numpy(WL.activations_f16(M, K, 60 + 4 * i + j, outlier_frac=0.01)).to(dev)
-             for j in range(len(names))]
-        svh = torch.from_numpy(WL.svh_scales(N, 70 + i)).to(dev)
-        skg = api.trellis_m256_skg(K, N, KB)
-        ws = torch.empty(api.lib().r4d_gemm_trellis_nt_m256_ws_bytes(M, N, skg) // 4, dtype=torch.float32, device=dev)
-        tk = api.TicketBuffer(N, dev).t
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
 
-        def run():
-            for c in range(copies):
-                if len(names) == 1:
-                    api.trellis_gemm_m256(a[0], words[c], svh, K, N, KB, skg=skg, out=out, ws=ws, tickets=tk,
-                                          out_scale=0.08838834764831845)
-                else:
-                    api.trellis_gemm_m256_parts(a, n0, words[c], svh, K, N, KB, skg=skg, out=out, ws=ws,
-                                                tickets=tk, out_scale=0.08838834764831845)
-        run()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            with torch.cuda.graph(g, stream=s):
-                for _ in range(R):
-                    run()
-        torch.cuda.synchronize()
-        g.replay()
-        st = torch.cuda.current_stream()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(st)
-        g.replay()
-        e1.record(st)
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / (R * copies)
-        flop = 2.0 * M * K * N
-        per_launch["|".join(names)] = {"us": round(ms * 1e3, 2), "TFLOPs": round(flop / (ms * 1e-3) / 1e12, 1),
-                                       "skg": skg}
-        tot_flop += flop
-        tot_ms += ms
-        del words
-        torch.cuda.empty_cache()
+    def layer(kb_of):
+        per_launch, tot_flop, tot_ms = {}, 0.0, 0.0
+        for i, (gname, members) in enumerate(WL.LAYER_GROUPS):
+            KBg = kb_of(gname)
+            names = [p for m in members for p in m]
+            K = shape[names[0]][0]
+            widths = [shape[p][1] for p in names]
+            N = sum(widths)
+            n0 = [int(v) for v in np.cumsum([0] + widths[:-1])]
+            nw = K * N * KBg // 32
+            copies = max(2, int(np.ceil(1.0e9 / (nw * 4))))
+            words = [torch.randint(-2**31, 2**31 - 1, (nw,), dtype=torch.int32, device=dev) for _ in range(copies)]
+            a = [torch.from_numpy(WL.activations_f16(M, K, 60 + 4 * i + j, outlier_frac=0.01)).to(dev)
+                 for j in range(len(names))]
+            svh = torch.from_numpy(WL.svh_scales(N, 70 + i)).to(dev)
+            skg = api.trellis_m256_skg(K, N, KBg)
+            ws = torch.empty(api.lib().r4d_gemm_trellis_nt_m256_ws_bytes(M, N, skg) // 4, dtype=torch.float32,
+                             device=dev)
+            tk = api.TicketBuffer(N, dev).t
+            out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+            def run():
+                for c in range(copies):
+                    if len(names) == 1:
+                        api.trellis_gemm_m256(a[0], words[c], svh, K, N, KBg, skg=skg, out=out, ws=ws, tickets=tk,
+                                              out_scale=0.08838834764831845)
+                    else:
+                        api.trellis_gemm_m256_parts(a, n0, words[c], svh, K, N, KBg, skg=skg, out=out, ws=ws,
+                                                    tickets=tk, out_scale=0.08838834764831845)
+            run()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(g, stream=s):
+                    for _ in range(R):
+                        run()
+            torch.cuda.synchronize()
+            g.replay()
+            st = torch.cuda.current_stream()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            g.replay()
+            e1.record(st)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / (R * copies)
+            flop = 2.0 * M * K * N
+            per_launch["|".join(names)] = {"us": round(ms * 1e3, 2), "TFLOPs": round(flop / (ms * 1e-3) / 1e12, 1),
+                                           "skg": skg, "KB": KBg}
+            tot_flop += flop
+            tot_ms += ms
+            del words, g
+            torch.cuda.empty_cache()
+        return per_launch, tot_flop, tot_ms
+
+    per_launch, tot_flop, tot_ms = layer(lambda g: KB)
+    rows = {}
+    if KB == 4:
+        for rate, kb_of in (("KB5", lambda g: 5), ("mix", lambda g: 5 if g in MIX_KB5 else 4)):
+            pl, fl, t = layer(kb_of)
+            rows[rate] = {"layer_us": round(t * 1e3, 1), "TFLOPs": round(fl / (t * 1e-3) / 1e12, 1),
+                          "per_launch_us": {k: v["us"] for k, v in pl.items()}}
     achieved = tot_flop / (tot_ms * 1e-3) / 1e12
     return {"metric": "M=256 trellis GEMM TFLOP/s (27B layer shapes, KB4)", "value": round(achieved, 1),
             "unit": "TFLOP/s", "roofline": {"bound": "mfma", "achieved": round(achieved, 1),
@@ -609,7 +624,9 @@ def bench_m256(api, WL, KB, R=3):
             "kernel": "tq_m256_kernel",
             "workload": "config2: the layer's 10 projections as 6 launches (same-input projections as one linear)",
             "layer_us": round(tot_ms * 1e3, 1), "per_launch": per_launch,
-            "per_projection_TFLOPs": round(per_proj, 1), "per_shape": per_shape}
+            "per_projection_TFLOPs": round(per_proj, 1), "per_shape": per_shape,
+            "rows": {"workload": "the same 6-launch layer at KB 5, and at config 1's 4/5 mix (GDN and attention at "
+                                 "KB 5, the MLP at KB 4)", "rows": rows}}
 
 
 def bench_w4a16(api, WL, R=8):
