@@ -650,17 +650,20 @@ def bench_w4a16(api, WL, R=8):
 
             def run(with_argmax):
                 for wq_d, wsz_d in copies:
+                    if with_argmax == "fused":
+                        api.w4a16_gemm_argmax(a, wq_d, wsz_d, K, N, g, out=out, out_idx=idx, out_val=val)
+                        continue
                     api.w4a16_gemm(a, wq_d, wsz_d, K, N, g, out=out, f32=True)
                     if with_argmax:
                         api.argmax_rows(out, idx, val)
-            # the argmax alone (one launch over the logits the GEMM left), the GEMM, and the GEMM with the argmax: three
-            # graphs, each replayed in three interleaved rounds (the median per graph), so that clock drift between
-            # measurements does not land on one of them
+            # the argmax alone (one launch over the logits the GEMM left), the GEMM, the GEMM with the argmax, and the
+            # fused entry (r4d_gemm_w4a16_nt_m64_f32_argmax): four graphs, each replayed in three interleaved rounds
+            # (the median per graph), so that clock drift between measurements does not land on one of them
             def run_am():
                 for _ in copies:
                     api.argmax_rows(out, idx, val)
             graphs = {}
-            for with_am in (None, False, True):
+            for with_am in (None, False, True, "fused"):
                 gr = torch.cuda.CUDAGraph()
                 s = torch.cuda.Stream()
                 s.wait_stream(torch.cuda.current_stream())
@@ -691,7 +694,8 @@ def bench_w4a16(api, WL, R=8):
                                  "GBs": round(nbytes / (times[False] * 1e-3) / 1e9, 1),
                                  "frac": round(nbytes / (times[False] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                  "gemm_plus_argmax_us": round(times[True] * 1e3, 2),
-                                 "argmax_alone_us": round(times[None] * 1e3, 2)}
+                                 "argmax_alone_us": round(times[None] * 1e3, 2),
+                                 "gemm_fused_argmax_us": round(times["fused"] * 1e3, 2)}
         del copies
         torch.cuda.empty_cache()
     return {"metric": "w4a16 LM head (N=248320, K=5120) effective HBM GB/s", "kernel": "w4_kernel",

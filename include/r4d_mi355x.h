@@ -144,6 +144,12 @@ void r4dx_argmax_val_bf16(int64_t logits, int64_t out_idx, int64_t out_val, int6
  * row r's result at out_idx[r * out_stride] (and out_val[r * out_stride] when out_val != 0). */
 void r4dx_argmax_rows_f32(int64_t logits, int64_t row_stride, int64_t out_idx, int64_t out_val,
                           int64_t out_stride, int64_t rows, int64_t vocab, int64_t stream);
+/* No reference counterpart (the LM head's GEMM and argmax in one launch, for the decode step that
+ * reads back only the token): r4d_gemm_w4a16_nt_m64_f32's logits c [M][N] plus r4dx_argmax_rows_f32's
+ * result per row, out_idx[m] and out_val[m] (out_val may be 0), bit for bit the two calls' results.
+ * Uses the same per-(device, stream) scratch as the argmax entries (first call not under capture). */
+void r4d_gemm_w4a16_nt_m64_f32_argmax(int group, int64_t a, int64_t wq, int64_t wsz, int64_t c, int64_t out_idx,
+                                      int64_t out_val, int M, int K, int N, int64_t stream);
 
 /* ---- int8 x int8 prefill GEMM and its activation quantizers ------------------------------------ */
 /* r4d.h:490-491 r4d_trellis_i8_quant_act: x f16 [256][K] (part p at x + p part_stride elements) -> the A8

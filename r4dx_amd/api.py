@@ -239,6 +239,34 @@ def w4a16_gemm(a, wq, wsz, K, N, group=64, out=None, f32=False, stream=None):
 _argmax_streams = set()   # (device, stream) pairs whose argmax scratch the library has allocated
 
 
+def _argmax_scratch_ready(device, st):
+    key = (device, st)
+    if key not in _argmax_streams and torch.cuda.is_current_stream_capturing():
+        # the library allocates a stream's argmax scratch at its first call, which graph capture forbids
+        raise ValueError("argmax: the stream's first argmax is under graph capture; run one on it before capturing")
+    _argmax_streams.add(key)
+
+
+def w4a16_gemm_argmax(a, wq, wsz, K, N, group=64, out=None, out_idx=None, out_val=None, stream=None):
+    """fp32 logits [M][N] and their per-row argmax (int32 [M], fp32 [M]) in one launch
+    (r4d_gemm_w4a16_nt_m64_f32_argmax)."""
+    L = lib()
+    M = a.shape[0]
+    msg = L.r4d_gemm_w4a16_nt_m64_check(group, M, K, N)
+    if msg:
+        raise ValueError(msg.decode())
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=a.device)
+    if out_idx is None:
+        out_idx = torch.empty(M, dtype=torch.int32, device=a.device)
+    if out_val is None:
+        out_val = torch.empty(M, dtype=torch.float32, device=a.device)
+    st = _stream(stream)
+    _argmax_scratch_ready(a.device.index, st)
+    L.r4d_gemm_w4a16_nt_m64_f32_argmax(group, _p(a), _p(wq), _p(wsz), _p(out), _p(out_idx), _p(out_val), M, K, N, st)
+    return out, out_idx, out_val
+
+
 def argmax_rows(logits, out_idx=None, out_val=None, stream=None):
     """Per-row argmax of a [rows][vocab] fp32 or bf16 tensor: (int32 [rows], fp32 [rows])."""
     L = lib()
@@ -250,11 +278,7 @@ def argmax_rows(logits, out_idx=None, out_val=None, stream=None):
     if not 1 <= rows <= 64 or vocab < 1:
         raise ValueError("argmax: rows must be 1..64 and vocab >= 1")
     st = _stream(stream)
-    key = (logits.device.index, st)
-    if key not in _argmax_streams and torch.cuda.is_current_stream_capturing():
-        # the library allocates a stream's argmax scratch at its first call, which graph capture forbids
-        raise ValueError("argmax: the stream's first argmax is under graph capture; run one on it before capturing")
-    _argmax_streams.add(key)
+    _argmax_scratch_ready(logits.device.index, st)
     if logits.dtype == torch.float32:
         L.r4dx_argmax_rows_f32(_p(logits), logits.stride(0), _p(out_idx), _p(out_val), 1, rows, vocab, st)
     elif logits.dtype == torch.bfloat16 and rows == 1:

@@ -97,12 +97,157 @@ __device__ __forceinline__ void w4_zeros(unsigned szw, unsigned& nz, unsigned& n
                                                                 (r4h2){(_Float16)15360.0f, (_Float16)15360.0f}));
 }
 
+// ---- argmax ------------------------------------------------------------------------------------------
+// (value, index) as one 64-bit key whose unsigned order is the reference's total order (larger value
+// first, then lower index; src/kernels/include/r4dx/kernels/argmax_ref.hpp:22-41): the value's bits made
+// order-preserving in the high word, the complemented index in the low word. A NaN gets key 0 (it never
+// wins); the seed (-inf, 0) is the key of an element (-inf, 0), so a row whose elements are all -inf or
+// NaN yields (-inf, 0). The maximum of keys is partition- and order-independent, so the multi-workgroup
+// reduction is exact and deterministic.
+__device__ __forceinline__ unsigned long long am_key(float v, unsigned idx) {
+  unsigned u = __builtin_bit_cast(unsigned, v);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0ull;
+  if ((u & 0x7FFFFFFFu) == 0u) u = 0u;                 // -0 == +0: equal values, the index decides
+  const unsigned ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)ord << 32) | (unsigned long long)(~idx);
+}
+__device__ __forceinline__ void am_decode(unsigned long long key, int* idx, float* val) {
+  const unsigned long long seed = am_key(-__builtin_inff(), 0u);
+  if (key < seed) key = seed;
+  const unsigned ord = (unsigned)(key >> 32);
+  const unsigned u = (ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord;
+  *idx = (int)(~(unsigned)key);
+  *val = __builtin_bit_cast(float, u);
+}
+__device__ __forceinline__ unsigned long long am_max(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+__device__ __forceinline__ unsigned long long am_wave_max(unsigned long long k) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const unsigned lo = __shfl_xor((unsigned)k, o, 64), hi = __shfl_xor((unsigned)(k >> 32), o, 64);
+    k = am_max(k, ((unsigned long long)hi << 32) | lo);
+  }
+  return k;
+}
+
+// The fused argmax of the logits entry: each workgroup reduces its columns to one key per row, folds it
+// into slot (workgroup mod kAmSlots) of the row with an atomic max, and takes the launch's ticket; the last
+// workgroup reduces the slots, writes (index, value) per row and clears the slots it read.
+constexpr int kAmSlots = 64;
+struct AmFused {
+  unsigned long long* slots;   // [kAmSlots][64 rows] u64, zero between launches
+  unsigned* ticket;            // one ticket line
+  int* out_idx;
+  float* out_val;              // may be null
+};
+
+// Epilogue of the fused argmax: the logits are stored coherently (agent scope, so the last workgroup reads
+// the winner's own bits whichever XCD wrote them); a wave reduces its lanes' keys per row across the lanes
+// that share the row, the workgroup across its waves in LDS, and one thread per row folds that into the
+// row's slot. Dead waves (no tile) and columns >= N contribute nothing.
+template <bool SMALL, int MT, typename Acc>
+__device__ __forceinline__ void w4_store_argmax(const Acc (&acc)[SMALL ? 1 : MT], float* __restrict__ C, int M,
+                                                int N, int t0, bool live, const AmFused& af) {
+  __shared__ unsigned long long red[kWaves][64];
+  __shared__ int flag;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lh = lane >> 5;
+  if constexpr (SMALL) {
+    // lane: column 16 (t0 + (e & 1)) + (lane & 15), row 2 (lane >> 4) + (e >> 1)
+    unsigned long long k[2] = {0ull, 0ull};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 2 * (lane >> 4) + (e >> 1), n = 16 * (t0 + (e & 1)) + (lane & 15);
+      if (live && m < M && n < N) {
+        __hip_atomic_store(&C[(size_t)m * N + n], acc[0][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        k[e >> 1] = am_max(k[e >> 1], am_key(acc[0][e], (unsigned)n));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const unsigned lo = __shfl_xor((unsigned)k[j], o, 64), hi = __shfl_xor((unsigned)(k[j] >> 32), o, 64);
+        k[j] = am_max(k[j], ((unsigned long long)hi << 32) | lo);
+      }
+      if ((lane & 15) == 0) red[w][2 * (lane >> 4) + j] = k[j];
+    }
+  } else {
+    // lane: column 16 t0 + (lane & 31), row i 32 + (e / 4) 8 + lh 4 + e % 4
+    const int n = 16 * t0 + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = i * 32 + (e >> 2) * 8 + lh * 4 + (e & 3);
+        unsigned long long k = 0ull;
+        if (live && m < M && n < N) {
+          __hip_atomic_store(&C[(size_t)m * N + n], acc[i][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          k = am_key(acc[i][e], (unsigned)n);
+        }
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) {
+          const unsigned lo = __shfl_xor((unsigned)k, o, 64), hi = __shfl_xor((unsigned)(k >> 32), o, 64);
+          k = am_max(k, ((unsigned long long)hi << 32) | lo);
+        }
+        if ((lane & 31) == 0) red[w][m] = k;
+      }
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < M) {
+    unsigned long long k = 0ull;
+#pragma unroll
+    for (int v = 0; v < kWaves; ++v) k = am_max(k, red[v][threadIdx.x]);
+    __hip_atomic_fetch_max(&af.slots[(blockIdx.x % kAmSlots) * 64 + threadIdx.x], k, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!r4_ticket_last(af.ticket, gridDim.x, &flag)) return;
+  // the last workgroup: thread t reads slot t / 8 of rows 8 j + t % 8 (all loads issued before any use),
+  // clears them, and the slots reduce across lanes (8 per wave) and waves
+  unsigned long long k[8];
+  const int sl = threadIdx.x >> 3, r8 = threadIdx.x & 7;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    k[j] = 8 * j + r8 < M ? __hip_atomic_load(&af.slots[sl * 64 + 8 * j + r8], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                          : 0ull;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (8 * j + r8 < M) __hip_atomic_store(&af.slots[sl * 64 + 8 * j + r8], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();   // every wave is past its reads of red
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (8 * j >= M) break;
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1) {
+      const unsigned lo = __shfl_xor((unsigned)k[j], o, 64), hi = __shfl_xor((unsigned)(k[j] >> 32), o, 64);
+      k[j] = am_max(k[j], ((unsigned long long)hi << 32) | lo);
+    }
+    if (lane < 8) red[w][8 * j + lane] = k[j];
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < M) {
+    const int row = threadIdx.x;
+    unsigned long long kr = 0ull;
+#pragma unroll
+    for (int v = 0; v < kWaves; ++v) kr = am_max(kr, red[v][row]);
+    int idx;
+    float val;
+    am_decode(kr, &idx, &val);
+    af.out_idx[row] = idx;
+    // the key holds the winner's bits except the sign of a zero: read a zero winner's own bits back
+    if (af.out_val)
+      af.out_val[row] = kr >= am_key(-__builtin_inff(), 0u) && val == 0.0f
+                            ? __hip_atomic_load(&C[(size_t)row * N + idx], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                            : val;
+  }
+}
+
 // SMALL: the 16x16x32 form (M <= 8). MT: row tiles of 32 in the 32x32x16 form.
-template <int G, bool SMALL, int MT, bool OUTF>
+// AM (with OUTF): the fused per-row argmax of the logits (AmFused).
+template <int G, bool SMALL, int MT, bool OUTF, bool AM>
 __global__ __launch_bounds__(64 * kWaves) void w4_kernel(const unsigned short* __restrict__ A,
                                                           const unsigned* __restrict__ Wq,
                                                           const unsigned* __restrict__ Wsz,
-                                                          void* __restrict__ Cv, int M, int K, int N) {
+                                                          void* __restrict__ Cv, int M, int K, int N, AmFused af) {
+  static_assert(!AM || OUTF, "the fused argmax reads fp32 logits");
   extern __shared__ r4u4 alds[];   // chunk fragments [kb][c][lh][M] of 8 halves, then a zero block
   const int lane = threadIdx.x & 63;
   const int KB64 = K >> 6, groups = K / G;
@@ -270,6 +415,10 @@ __global__ __launch_bounds__(64 * kWaves) void w4_kernel(const unsigned short* _
     for (int i = 0; i < kPF; ++i)
       if (full + i < KB64) compute(ring[i], full - kb_chunk + i);
   }
+  if constexpr (AM) {
+    w4_store_argmax<SMALL, MT>(acc, (float*)Cv, M, N, t0, live, af);
+    return;
+  }
   if (!live) return;
 
   if constexpr (SMALL) {
@@ -309,8 +458,8 @@ std::string w4_check(int group, int M, int K, int N) {
   return "";
 }
 
-template <int G, bool OUTF>
-void w4_launch(int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int N, hipStream_t st) {
+template <int G, bool OUTF, bool AM>
+void w4_launch(int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int N, hipStream_t st, const AmFused& af) {
   const int tiles = N / 16;
   const int waves = (tiles + 1) / 2;
   dim3 grid((waves + kWaves - 1) / kWaves), block(64 * kWaves);
@@ -318,9 +467,9 @@ void w4_launch(int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int 
   auto Ap = (const unsigned short*)a;
   auto Wp = (const unsigned*)wq;
   auto Sp = (const unsigned*)wsz;
-  if (M <= 8) hipLaunchKernelGGL((w4_kernel<G, true, 1, OUTF>), grid, block, smem, st, Ap, Wp, Sp, (void*)c, M, K, N);
-  else if (M <= 32) hipLaunchKernelGGL((w4_kernel<G, false, 1, OUTF>), grid, block, smem, st, Ap, Wp, Sp, (void*)c, M, K, N);
-  else hipLaunchKernelGGL((w4_kernel<G, false, 2, OUTF>), grid, block, smem, st, Ap, Wp, Sp, (void*)c, M, K, N);
+  if (M <= 8) hipLaunchKernelGGL((w4_kernel<G, true, 1, OUTF, AM>), grid, block, smem, st, Ap, Wp, Sp, (void*)c, M, K, N, af);
+  else if (M <= 32) hipLaunchKernelGGL((w4_kernel<G, false, 1, OUTF, AM>), grid, block, smem, st, Ap, Wp, Sp, (void*)c, M, K, N, af);
+  else hipLaunchKernelGGL((w4_kernel<G, false, 2, OUTF, AM>), grid, block, smem, st, Ap, Wp, Sp, (void*)c, M, K, N, af);
 }
 
 void w4_run(int group, int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int N, bool outf,
@@ -328,46 +477,15 @@ void w4_run(int group, int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int
   r4d::require(entry, w4_check(group, M, K, N));
   if (!a || !wq || !wsz || !c) r4d::fail(entry, "null buffer");
   hipStream_t st = (hipStream_t)stream;
+  const AmFused none{nullptr, nullptr, nullptr, nullptr};
   if (group == 32) {
-    if (outf) w4_launch<32, true>(a, wq, wsz, c, M, K, N, st);
-    else w4_launch<32, false>(a, wq, wsz, c, M, K, N, st);
+    if (outf) w4_launch<32, true, false>(a, wq, wsz, c, M, K, N, st, none);
+    else w4_launch<32, false, false>(a, wq, wsz, c, M, K, N, st, none);
   } else {
-    if (outf) w4_launch<64, true>(a, wq, wsz, c, M, K, N, st);
-    else w4_launch<64, false>(a, wq, wsz, c, M, K, N, st);
+    if (outf) w4_launch<64, true, false>(a, wq, wsz, c, M, K, N, st, none);
+    else w4_launch<64, false, false>(a, wq, wsz, c, M, K, N, st, none);
   }
   r4d::launch_ok(entry);
-}
-
-// ---- argmax ------------------------------------------------------------------------------------------
-// (value, index) as one 64-bit key whose unsigned order is the reference's total order (larger value
-// first, then lower index; src/kernels/include/r4dx/kernels/argmax_ref.hpp:22-41): the value's bits made
-// order-preserving in the high word, the complemented index in the low word. A NaN gets key 0 (it never
-// wins); the seed (-inf, 0) is the key of an element (-inf, 0), so a row whose elements are all -inf or
-// NaN yields (-inf, 0). The maximum of keys is partition- and order-independent, so the multi-workgroup
-// reduction is exact and deterministic.
-__device__ __forceinline__ unsigned long long am_key(float v, unsigned idx) {
-  unsigned u = __builtin_bit_cast(unsigned, v);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0ull;
-  if ((u & 0x7FFFFFFFu) == 0u) u = 0u;                 // -0 == +0: equal values, the index decides
-  const unsigned ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((unsigned long long)ord << 32) | (unsigned long long)(~idx);
-}
-__device__ __forceinline__ void am_decode(unsigned long long key, int* idx, float* val) {
-  const unsigned long long seed = am_key(-__builtin_inff(), 0u);
-  if (key < seed) key = seed;
-  const unsigned ord = (unsigned)(key >> 32);
-  const unsigned u = (ord & 0x80000000u) ? (ord & 0x7FFFFFFFu) : ~ord;
-  *idx = (int)(~(unsigned)key);
-  *val = __builtin_bit_cast(float, u);
-}
-__device__ __forceinline__ unsigned long long am_max(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
-__device__ __forceinline__ unsigned long long am_wave_max(unsigned long long k) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const unsigned lo = __shfl_xor((unsigned)k, o, 64), hi = __shfl_xor((unsigned)(k >> 32), o, 64);
-    k = am_max(k, ((unsigned long long)hi << 32) | lo);
-  }
-  return k;
 }
 
 constexpr int kAmParts = 256;         // most workgroups per row (partial keys per row)
@@ -377,12 +495,17 @@ constexpr int kAmThreads = 256;
 
 // Partial keys of one argmax: [kAmMaxRows][kAmParts] u64, then a ticket line (R4_TICKET_WORDS u32) per row. Each
 // row's workgroups store their keys, take the row's ticket, and the last one reduces the row and resets the ticket.
+// The fused argmax of the logits entry has a region of its own after these: kAmSlots x kAmMaxRows u64 slots and one
+// ticket line (AmFused).
 struct AmScratch {
   unsigned long long* keys;
   unsigned* tickets;
+  unsigned long long* fused_slots;
+  unsigned* fused_ticket;
 };
 constexpr size_t kAmScratchBytes =
-    (size_t)kAmMaxRows * kAmParts * sizeof(unsigned long long) + (size_t)kAmMaxRows * R4_TICKET_WORDS * sizeof(unsigned);
+    (size_t)kAmMaxRows * kAmParts * sizeof(unsigned long long) + (size_t)kAmMaxRows * R4_TICKET_WORDS * sizeof(unsigned) +
+    (size_t)kAmSlots * kAmMaxRows * sizeof(unsigned long long) + R4_TICKET_WORDS * sizeof(unsigned);
 
 // One launch: workgroup (b, row) reduces elements [b chunk, (b + 1) chunk) of its row to one key; the last of the
 // row's nblk workgroups (ticket) reduces their keys in a fixed order and writes the result.
@@ -458,6 +581,8 @@ AmScratch am_scratch(hipStream_t st, const char* entry) {
   AmScratch s;
   s.keys = (unsigned long long*)it->second;
   s.tickets = (unsigned*)(s.keys + (size_t)kAmMaxRows * kAmParts);
+  s.fused_slots = (unsigned long long*)(s.tickets + (size_t)kAmMaxRows * R4_TICKET_WORDS);
+  s.fused_ticket = (unsigned*)(s.fused_slots + (size_t)kAmSlots * kAmMaxRows);
   return s;
 }
 
@@ -481,6 +606,18 @@ void am_run(bool bf16, int64_t x, int64_t row_stride, int64_t out_idx, int64_t o
   else hipLaunchKernelGGL(am_kernel<false>, grid, dim3(kAmThreads), 0, st, (const void*)x, (long long)row_stride,
                           (long long)vocab, chunk, (int)nblk, sc, (int*)out_idx, (float*)out_val,
                           (long long)out_stride);
+  r4d::launch_ok(entry);
+}
+
+void w4_argmax_run(int group, int64_t a, int64_t wq, int64_t wsz, int64_t c, int64_t out_idx, int64_t out_val, int M,
+                   int K, int N, int64_t stream, const char* entry) {
+  r4d::require(entry, w4_check(group, M, K, N));
+  if (!a || !wq || !wsz || !c || !out_idx) r4d::fail(entry, "null buffer");
+  hipStream_t st = (hipStream_t)stream;
+  const AmScratch sc = am_scratch(st, entry);
+  const AmFused af{sc.fused_slots, sc.fused_ticket, (int*)out_idx, (float*)out_val};
+  if (group == 32) w4_launch<32, true, true>(a, wq, wsz, c, M, K, N, st, af);
+  else w4_launch<64, true, true>(a, wq, wsz, c, M, K, N, st, af);
   r4d::launch_ok(entry);
 }
 
@@ -509,6 +646,11 @@ const char* r4d_gemm_w4a16_nt_m64_check(int group, int M, int K, int N) {
 void r4d_gemm_w4a16_nt_m64_f32(int group, int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int N,
                                int64_t stream) {
   w4_run(group, a, wq, wsz, c, M, K, N, true, stream, "gemm_w4a16_nt_m64_f32");
+}
+
+void r4d_gemm_w4a16_nt_m64_f32_argmax(int group, int64_t a, int64_t wq, int64_t wsz, int64_t c, int64_t out_idx,
+                                      int64_t out_val, int M, int K, int N, int64_t stream) {
+  w4_argmax_run(group, a, wq, wsz, c, out_idx, out_val, M, K, N, stream, "gemm_w4a16_nt_m64_f32_argmax");
 }
 
 void r4dx_argmax_f32(int64_t logits, int64_t out_idx, int64_t vocab, int64_t stream) {

@@ -40,6 +40,7 @@ SIGS = {
     "r4dx_argmax_bf16": (None, [I64, I64, I64, I64]),
     "r4dx_argmax_val_bf16": (None, [I64, I64, I64, I64, I64]),
     "r4dx_argmax_rows_f32": (None, [I64] * 8),
+    "r4d_gemm_w4a16_nt_m64_f32_argmax": (None, [I32, I64, I64, I64, I64, I64, I64, I32, I32, I32, I64]),
     "r4d_trellis_i8_quant_act": (None, [I64, I64, I64, I32, I64, I32, I64]),
     "r4d_trellis_i8_quant_act_row": (None, [I64, I64, I64, I32, I64, I32, I64]),
     "r4d_i8_quant_act_plain": (None, [I64, I64, I64, I32, I32, I32, I64]),
