@@ -3,7 +3,8 @@ bit-identical to r4d_gemm_w4a16_nt_m64_f32's on the same inputs, and its (index,
 oracle's argmax order (larger value first, then lower index, NaN never wins) over those logits -- so to the two-call
 GEMM + r4dx_argmax_rows_f32 path. Cases: both MFMA forms and both row-tile counts, spare waves (N not a multiple of
 the 256 columns of a workgroup), the full config-3 vocab, planted ties across workgroups, NaN and all-zero rows, and
-back-to-back calls on one stream (the slots and the ticket clear themselves) with a smaller second call."""
+back-to-back calls on one stream (the slots and the ticket clear themselves) with a smaller second call, HIP-graph
+replays with eager calls between them, and two streams at once."""
 import ctypes as C
 
 import numpy as np
@@ -91,3 +92,60 @@ def test_fused_argmax_ties_nan_zero():
     twin = t_dst * 16 + win % 16
     assert _bits(logits2[0, twin]) == _bits(logits2[0, win])
     assert int(idx2[0]) == min(win, twin)
+
+
+def test_fused_argmax_graph_replays_and_two_streams():
+    """Captured in a HIP graph and replayed three times with eager launches between the replays (the slots and the
+    ticket must be clear at every replay), each replay against the eager result; then two streams running the entry
+    at once on different inputs (each stream has its own slots and ticket)."""
+    group, N, K = 64, 16384, 2048
+    wq, wsz = WL.w4a16_packed(N, K, group, 51)
+    a = WL.activations_f16(8, K, 52).view(np.uint16)
+    b = WL.activations_f16(8, K, 53).view(np.uint16)
+    wq_d, wsz_d, a_d, b_d = dev(wq), dev(wsz), dev(a), dev(b)
+    banner("w4a16 argmax graph")
+    c_ref, i_ref, v_ref = api.w4a16_gemm_argmax(a_d, wq_d, wsz_d, K, N, group)
+    torch.cuda.synchronize()
+    i_ref, v_ref = i_ref.cpu().numpy(), v_ref.cpu().numpy()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    out = torch.empty((8, N), dtype=torch.float32, device="cuda")
+    idx = torch.empty(8, dtype=torch.int32, device="cuda")
+    val = torch.empty(8, dtype=torch.float32, device="cuda")
+    with torch.cuda.stream(s):
+        api.w4a16_gemm_argmax(a_d, wq_d, wsz_d, K, N, group, out=out, out_idx=idx, out_val=val)   # scratch of s
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            api.w4a16_gemm_argmax(a_d, wq_d, wsz_d, K, N, group, out=out, out_idx=idx, out_val=val)
+    torch.cuda.synchronize()
+    for r in range(3):
+        idx.fill_(-1)
+        val.fill_(0.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(idx.cpu().numpy(), i_ref), r
+        assert np.array_equal(_bits(val.cpu().numpy()), _bits(v_ref)), r
+        # eager work between the replays, on the same stream's scratch and on the default stream's
+        with torch.cuda.stream(s):
+            api.w4a16_gemm_argmax(b_d[:3], wq_d, wsz_d, K, N, group)
+        api.w4a16_gemm_argmax(b_d[:5], wq_d, wsz_d, K, N, group)
+        torch.cuda.synchronize()
+    banner("w4a16 argmax two streams")
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for st in (s1, s2):
+        with torch.cuda.stream(st):
+            api.w4a16_gemm_argmax(a_d[:1], wq_d, wsz_d, K, N, group)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            ca, ia, va = api.w4a16_gemm_argmax(a_d, wq_d, wsz_d, K, N, group)
+        with torch.cuda.stream(s2):
+            cb, ib, vb = api.w4a16_gemm_argmax(b_d, wq_d, wsz_d, K, N, group)
+        torch.cuda.synchronize()
+        for c, i, v in ((ca, ia, va), (cb, ib, vb)):
+            logits = c.cpu().numpy()
+            for m in range(8):
+                vv = C.c_float()
+                assert int(i[m]) == O.lib().r4o_argmax_f32(ptr(np.ascontiguousarray(logits[m])), N, C.byref(vv))
+                assert _bits(v[m].item()) == _bits(vv.value)
