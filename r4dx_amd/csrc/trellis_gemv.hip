@@ -98,9 +98,16 @@ constexpr int kRedRows = 4;          // rows of the final slice sum per pass (8 
 // n / d for the staging loops' row split (d = M <= 64, n below 2^20): one high multiply by the launch-uniform
 // floor(2^32 / d) + 1, exact whenever n d < 2^32 (the error term n e / (d 2^32), 0 < e <= d, stays below 1 / d);
 // d = 1 (whose multiplier would need 33 bits) is marked by 0 and returns n.
-__device__ __forceinline__ unsigned r4_div_magic(unsigned d) {
-  return d == 1u ? 0u : (unsigned)(0x100000000ull / d) + 1u;
-}
+// The multipliers for d = 0..64 as a constant table (d = 0 unused): a scalar load of the launch's M instead of a 64-bit
+// division formed with VALU ops in every wave.
+struct R4DivMagic {
+  unsigned m[65];
+  constexpr R4DivMagic() : m() {
+    for (unsigned d = 1; d <= 64; ++d) m[d] = d == 1u ? 0u : (unsigned)(0x100000000ull / d) + 1u;
+  }
+};
+__constant__ constexpr R4DivMagic kR4DivMagic{};
+__device__ __forceinline__ unsigned r4_div_magic(unsigned d) { return kR4DivMagic.m[d]; }
 __device__ __forceinline__ int r4_div_by(int n, unsigned magic) {
   return magic ? (int)__umulhi((unsigned)n, magic) : n;
 }
@@ -135,7 +142,7 @@ __global__ __launch_bounds__(64 * NPW * SK) void tq_gemv_kernel(
   const int ky = blockIdx.y;
   const int pair = blockIdx.x * NPW + pl;
   const int group = (blockIdx.x * NPW) >> 2;
-  const int KT = K >> 4, ktw = KT / SKG, kt0 = ky * ktw;
+  const int KT = K >> 4, ktw = r4_div_by(KT, r4_div_magic((unsigned)SKG)), kt0 = ky * ktw;   // SKG <= 64, KT < 2^20
   const unsigned short* __restrict__ A0 = ap.a[0];
   const unsigned short* __restrict__ A = r4_part_a(ap, group * 128);
   const int q = lane >> 4, t = (lane >> 3) & 1, c = lane & 7, mrow = lane & 15;
