@@ -1,7 +1,7 @@
 """r4dx_gemm_trellis_nt_m64_noalloc (the GEMV with its split-K partials and tickets in the library's own device
 array) against r4d_gemm_trellis_nt_m64 with caller buffers, through the C ABI: two calls in a row, the second with
-a smaller input, both byte-identical to the existing entry at the same (SK, SKG); and its size rule refuses what the
-array cannot hold."""
+a smaller input, both byte-identical to the existing entry at the same (SK, SKG); its size rule refuses what the
+array cannot hold; and a captured call replays byte-identically with eager calls between the replays."""
 import ctypes as C
 
 import numpy as np
@@ -69,3 +69,35 @@ def test_noalloc_size_rule():
     assert b"exceed the scratch" in ck(64, 5120, 8192 + 128, 8192 + 128, 4, 8)
     assert b"exceed the scratch" in ck(64, 5120, 34816, 34816, 4, 8)    # 71 MB
     assert b"N must be at most" in ck(1, 5120, 262144 + 128, 262144 + 128, 4, 1)
+
+
+def test_noalloc_graph_replays():
+    """The callers this entry is for capture it: a graph of one call (split, SKG 4) replayed three times with eager
+    calls of the entry on another input between the replays (the array's tickets must be back at zero every time),
+    each replay byte-identical to the eager call."""
+    L, f, ck = _entry()
+    K, N, KB, M, SK, skg = 2048, 1024, 4, 2, 0, 4
+    banner("noalloc graph", K, N, M, skg)
+    words, _, svh = WL.trellis_linear(K, N, KB, 61)
+    w_d, svh_d = dev(words), dev(svh)
+    a = [dev(WL.activations_f16(M, K, 62 + v).view(np.uint16)) for v in (0, 1)]
+    out = [torch.empty((M, N), dtype=torch.bfloat16, device="cuda") for _ in (0, 1)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _noalloc(f, ck, a[0], w_d, svh_d, K, N, KB, SK, skg, out[0])
+        torch.cuda.synchronize()
+        want = host_u16(out[0]).copy()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            _noalloc(f, ck, a[0], w_d, svh_d, K, N, KB, SK, skg, out[0])
+    torch.cuda.synchronize()
+    for r in range(3):
+        out[0].zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host_u16(out[0]), want), r
+        with torch.cuda.stream(s):
+            _noalloc(f, ck, a[1], w_d, svh_d, K, N, KB, SK, skg, out[1])
+        torch.cuda.synchronize()
