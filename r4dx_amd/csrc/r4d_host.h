@@ -55,6 +55,10 @@ inline std::string str(long long v) { return std::to_string(v); }
 void launch_split_finish(const float* ws, const float* svh, void* c, int M, int N, int SKG, int full, float out_scale,
                          hipStream_t st);
 
+// Zeroes `bytes` bytes at p (4-byte aligned) with a fill kernel on st, ordered with the stream's other work and
+// recordable in a HIP graph (no memset node); a launch failure thrown naming `entry`.
+void launch_clear(void* p, size_t bytes, hipStream_t st, const char* entry);
+
 }  // namespace r4d
 
 // Arguments of one trellis GEMV launch (trellis_gemv.hip).

@@ -769,6 +769,25 @@ void r4d::gemv_run(r4d_gemv_args& a, const char* entry) {
   r4d::launch_ok(entry);
 }
 
+// Grid-stride zero fill of `words` u32 words and `tail` (0..3) trailing bytes.
+__global__ __launch_bounds__(256) void r4_clear_kernel(unsigned* __restrict__ p, size_t words, int tail) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < words; i += stride) p[i] = 0u;
+  if (blockIdx.x == 0 && (int)threadIdx.x < tail) ((unsigned char*)(p + words))[threadIdx.x] = 0;
+}
+
+namespace r4d {
+void launch_clear(void* p, size_t bytes, hipStream_t st, const char* entry) {
+  if (bytes == 0) return;
+  const size_t words = bytes / 4;
+  size_t blocks = (words + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 1024) blocks = 1024;
+  hipLaunchKernelGGL(r4_clear_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (unsigned*)p, words, (int)(bytes & 3));
+  launch_ok(entry);
+}
+}  // namespace r4d
+
 extern "C" {
 
 const char* r4d_gemm_trellis_nt_m64_check(int M, int K, int N, int n_split, int KB, int SKG,
@@ -970,8 +989,8 @@ size_t r4d_gemm_trellis_nt_m64_tickets_bytes(int N) {
 void r4d_gemm_trellis_nt_m64_zero_tickets(int64_t tickets, size_t bytes, int64_t stream) {
   if (bytes == 0) return;
   if (tickets == 0) r4d::fail("gemm_trellis_nt_m64_zero_tickets", "null buffer");
-  const hipError_t e = hipMemsetAsync((void*)tickets, 0, bytes, (hipStream_t)stream);
-  if (e != hipSuccess) r4d::fail("gemm_trellis_nt_m64_zero_tickets", hipGetErrorString(e));
+  if (tickets & 3) r4d::fail("gemm_trellis_nt_m64_zero_tickets", "tickets must be 4-byte aligned");
+  r4d::launch_clear((void*)tickets, bytes, (hipStream_t)stream, "gemm_trellis_nt_m64_zero_tickets");
 }
 
 void r4d_trellis_reconstruct_f16(int64_t w, int64_t q, int K, int N, int KB, int64_t stream) {

@@ -315,9 +315,16 @@ __global__ __launch_bounds__(64 * kWaves) void w4_kernel(const unsigned short* _
 #pragma unroll
   for (int i = 0; i < NA; ++i) acc[i] = Acc{};
 
+  // COOP (the 16x16x32 form at G = 32): the wave's 64 scale words of a block -- (tile t0 + (lane >> 5), group
+  // (lane >> 4) & 1, column lane & 15) -- one load per lane instead of four, each handed to the lanes that use it at
+  // compute time (ds_bpermute). Measured: g32 M = 1 / 8 146 -> 144 / 155 -> 151 us; at G = 64 (two loads replaced)
+  // 5 % slower, so G = 64 keeps its own loads.
+  constexpr bool COOP = SMALL && G == 32;
+  const unsigned coop_base = (unsigned)((((size_t)(t0 + (lane >> 5)) * groups + (NG == 2 ? (lane >> 4) & 1 : 0)) * 16 +
+                                         (lane & 15)) * 4u);
   struct St {
     r4u4 w;
-    unsigned sz[NG * NS];
+    unsigned sz[COOP ? 1 : NG * NS];
   };
   auto load = [&](St& s, int kb) {
     const int kc = kb < KB64 ? kb : KB64 - 1;
@@ -325,7 +332,9 @@ __global__ __launch_bounds__(64 * kWaves) void w4_kernel(const unsigned short* _
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       const unsigned go = (unsigned)(NG * kc + g) * 64u;
-      if constexpr (SMALL) {
+      if constexpr (COOP) {
+        if (g == 0) s.sz[0] = __builtin_amdgcn_raw_buffer_load_b32(sr, coop_base + (unsigned)(NG * kc) * 64u, 0, kNT);
+      } else if constexpr (SMALL) {
         s.sz[2 * g] = __builtin_amdgcn_raw_buffer_load_b32(sr, st0 + go, 0, kNT);
         s.sz[2 * g + 1] = __builtin_amdgcn_raw_buffer_load_b32(sr, st1 + go, 0, kNT);
       } else {
@@ -333,7 +342,22 @@ __global__ __launch_bounds__(64 * kWaves) void w4_kernel(const unsigned short* _
       }
     }
   };
-  auto compute = [&](const St& s, int kbl) {
+  auto compute = [&](const St& s0, int kbl) {
+    // the block's scale words of the lane's column: word 2 g + t for group g, tile t0 + t (COOP: from the lanes that
+    // loaded them)
+    unsigned szl[NG * NS];
+    if constexpr (COOP) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          szl[2 * g + t] = (unsigned)__builtin_amdgcn_ds_bpermute(((t << 5) | (g << 4) | (lane & 15)) << 2, (int)s0.sz[0]);
+    }
+    struct SzView {
+      const unsigned* p;
+      __device__ unsigned operator[](int i) const { return p[i]; }
+    };
+    const struct { SzView sz; } s{SzView{COOP ? szl : s0.sz}};
     unsigned nz[4], nz16[4];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
@@ -344,7 +368,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4_kernel(const unsigned short* _
       for (int q = 0; q < 4 / NG; ++q) { nz[g * (4 / NG) + q] = a; nz16[g * (4 / NG) + q] = b; }
     }
     W4B bq;
-    w4_dequant(s.w, nz, nz16, bq);
+    w4_dequant(s0.w, nz, nz16, bq);
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       // group g: G = 64 -> U chain (c 0, 1), S chain (c 2, 3); G = 32 -> g 0: c 0 / 2, g 1: c 1 / 3
@@ -557,7 +581,7 @@ __global__ __launch_bounds__(kAmThreads) void am_kernel(const void* __restrict__
   }
 }
 
-// The scratch of one (device, stream): allocated and zeroed at the stream's first argmax, kept for the process
+// The scratch of one (device, stream): allocated and zeroed on that stream at its first argmax, kept for the process
 // (the reference keeps its argmax partials per stream the same way, src/kernels/src/r4dx_kernels.hip:1715-1734),
 // so argmax calls on different streams of one device -- an MTP head beside its model -- never share partials.
 // A first call on a stream under graph capture cannot allocate and throws: run one argmax on that stream first.
@@ -575,7 +599,8 @@ AmScratch am_scratch(hipStream_t st, const char* entry) {
                        "run one argmax on this stream before capturing");
     void* p = nullptr;
     if (hipMalloc(&p, kAmScratchBytes) != hipSuccess) r4d::fail(entry, "scratch allocation failed");
-    if (hipMemset(p, 0, kAmScratchBytes) != hipSuccess) r4d::fail(entry, "scratch clear failed");
+    // cleared on st itself: a null-stream memset is not ordered with a non-blocking stream's next kernel
+    r4d::launch_clear(p, kAmScratchBytes, st, entry);
     it = by_stream.emplace(std::make_pair(dev, st), p).first;
   }
   AmScratch s;

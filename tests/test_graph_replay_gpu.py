@@ -46,8 +46,11 @@ def _replays(name, run, out_of):
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
-        for t, w in zip(out_of(0), want):
-            assert np.array_equal(_bits(t), w), (name, r)
+        for j, (t, w) in enumerate(zip(out_of(0), want)):
+            got = _bits(t)
+            bad = np.flatnonzero(got.reshape(-1) != w.reshape(-1))
+            assert bad.size == 0, (name, r, j, int(bad.size), bad[:8].tolist(), got.reshape(-1)[bad[:4]].tolist(),
+                                   w.reshape(-1)[bad[:4]].tolist())
         with torch.cuda.stream(s):
             run(1)                               # eager work between the replays, the same ws and tickets
         torch.cuda.synchronize()
