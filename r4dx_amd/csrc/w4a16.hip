@@ -144,11 +144,19 @@ struct AmFused {
 // the winner's own bits whichever XCD wrote them); a wave reduces its lanes' keys per row across the lanes
 // that share the row, the workgroup across its waves in LDS, and one thread per row folds that into the
 // row's slot. Dead waves (no tile) and columns >= N contribute nothing.
+// The per-wave keys and the ticket flag reuse the A chunk's LDS (w4_am_lds bytes of it): a static array would
+// take the M = 8 workgroup past 40 KiB and the CU from four workgroups to three.
+template <bool SMALL>
+constexpr int w4_am_rows() { return SMALL ? 8 : 64; }
+__host__ __device__ constexpr size_t w4_am_lds(bool small) { return (size_t)kWaves * (small ? 8 : 64) * 8 + 16; }
+
 template <bool SMALL, int MT, typename Acc>
 __device__ __forceinline__ void w4_store_argmax(const Acc (&acc)[SMALL ? 1 : MT], float* __restrict__ C, int M,
-                                                int N, int t0, bool live, const AmFused& af) {
-  __shared__ unsigned long long red[kWaves][64];
-  __shared__ int flag;
+                                                int N, int t0, bool live, const AmFused& af, void* lds) {
+  constexpr int RS = w4_am_rows<SMALL>();
+  auto red = reinterpret_cast<unsigned long long (*)[RS]>(lds);
+  int* flag = reinterpret_cast<int*>(red + kWaves);
+  __syncthreads();   // every wave is past its last read of the A chunk
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lh = lane >> 5;
   if constexpr (SMALL) {
     // lane: column 16 (t0 + (e & 1)) + (lane & 15), row 2 (lane >> 4) + (e >> 1)
@@ -199,7 +207,7 @@ __device__ __forceinline__ void w4_store_argmax(const Acc (&acc)[SMALL ? 1 : MT]
     __hip_atomic_fetch_max(&af.slots[(blockIdx.x % kAmSlots) * 64 + threadIdx.x], k, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (!r4_ticket_last(af.ticket, gridDim.x, &flag)) return;
+  if (!r4_ticket_last(af.ticket, gridDim.x, flag)) return;
   // the last workgroup: thread t reads slot t / 8 of rows 8 j + t % 8 (all loads issued before any use),
   // clears them, and the slots reduce across lanes (8 per wave) and waves
   unsigned long long k[8];
@@ -440,7 +448,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4_kernel(const unsigned short* _
       if (full + i < KB64) compute(ring[i], full - kb_chunk + i);
   }
   if constexpr (AM) {
-    w4_store_argmax<SMALL, MT>(acc, (float*)Cv, M, N, t0, live, af);
+    w4_store_argmax<SMALL, MT>(acc, (float*)Cv, M, N, t0, live, af, (void*)alds);
     return;
   }
   if (!live) return;
@@ -487,7 +495,8 @@ void w4_launch(int64_t a, int64_t wq, int64_t wsz, int64_t c, int M, int K, int 
   const int tiles = N / 16;
   const int waves = (tiles + 1) / 2;
   dim3 grid((waves + kWaves - 1) / kWaves), block(64 * kWaves);
-  const size_t smem = (size_t)w4_chunk(M, K / 64, w4_pf(G, M <= 8)) * 8 * (M + 1) * 16;
+  size_t smem = (size_t)w4_chunk(M, K / 64, w4_pf(G, M <= 8)) * 8 * (M + 1) * 16;
+  if (AM && smem < w4_am_lds(M <= 8)) smem = w4_am_lds(M <= 8);
   auto Ap = (const unsigned short*)a;
   auto Wp = (const unsigned*)wq;
   auto Sp = (const unsigned*)wsz;
