@@ -44,7 +44,8 @@ int    r4d_gemm_trellis_nt_m64_has_rate(int KB);                 /* r4d.h:384 */
 int    r4d_gemm_trellis_nt_m64_max_m(void);                      /* r4d.h:385 */
 size_t r4d_gemm_trellis_nt_m64_ws_bytes(int M, int N, int SKG);  /* r4d.h:386 */
 size_t r4d_gemm_trellis_nt_m64_tickets_bytes(int N);             /* r4d.h:387: N/128 lines of 128 B */
-void   r4d_gemm_trellis_nt_m64_zero_tickets(int64_t tickets, size_t bytes, int64_t stream); /* r4d.h:389 */
+/* r4d.h:389. Zeroes with a fill kernel on `stream` (no memset node: graph-capturable); tickets 4-byte aligned. */
+void   r4d_gemm_trellis_nt_m64_zero_tickets(int64_t tickets, size_t bytes, int64_t stream);
 /* r4d.h:390-393: the whole decoded Q[K][N] f16 bits, bit-exact against the format's decode. */
 void   r4d_trellis_reconstruct_f16(int64_t w, int64_t q, int K, int N, int KB, int64_t stream);
 /* No reference counterpart (the reference checks inside the throwing entry, r4d_gemm_trellis_nt_m64.hip:
