@@ -140,3 +140,52 @@ def test_graph_w4a16_and_argmax():
         api.w4a16_gemm(a[v], wq_d, wsz_d, K, N, group, out=out[v], f32=True)
         api.argmax_rows(out[v], idx[v], val[v])
     _replays("w4a16 + argmax", run, lambda v: [out[v], idx[v], val[v]])
+
+
+def test_graph_zero_tickets_then_split_gemv():
+    """r4d_gemm_trellis_nt_m64_zero_tickets captured with the split launch that follows it (the engine's recovery
+    sequence): the clear is a kernel node, so every replay starts from zeroed tickets although the buffer is
+    poisoned before each one; every replay's output equals the eager launch on a fresh buffer."""
+    K, N, M, skg = 6144, 5120, 4, 4
+    words, _, svh = WL.trellis_linear(K, N, KB, 61)
+    w_d, svh_d = dev(words), dev(svh)
+    a = dev(WL.activations_f16(M, K, 62).view(np.uint16))
+    want = _bits(api.trellis_gemm_m64(a, w_d, svh_d, K, N, KB, skg=skg, out_scale=OUT_SCALE))
+    tk = api.TicketBuffer(N).t
+    nbytes = api.lib().r4d_gemm_trellis_nt_m64_tickets_bytes(N)
+    ws = torch.empty(api.lib().r4d_gemm_trellis_nt_m64_ws_bytes(M, N, skg) // 4, dtype=torch.float32, device="cuda")
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    banner("graph", "zero_tickets + split GEMV")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+
+    def run():
+        api.lib().r4d_gemm_trellis_nt_m64_zero_tickets(tk.data_ptr(), nbytes, torch.cuda.current_stream().cuda_stream)
+        api.trellis_gemm_m64(a, w_d, svh_d, K, N, KB, skg=skg, out=out, ws=ws, tickets=tk, out_scale=OUT_SCALE)
+    with torch.cuda.stream(s):
+        run()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            run()
+    torch.cuda.synchronize()
+    for r in range(3):
+        tk.copy_(torch.randint(1, 1 << 20, tk.shape, dtype=torch.int32, device="cuda"))
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(out), want), r
+        assert int(tk.abs().sum()) == 0, r
+
+
+def test_zero_tickets_byte_tail():
+    """The clear covers exactly `bytes` bytes, a tail of 1-3 bytes past the last whole word included."""
+    banner("zero_tickets tail")
+    buf = torch.full((64,), 0x5A, dtype=torch.uint8, device="cuda")
+    for nb in (1, 4, 7, 13, 60):
+        buf.fill_(0x5A)
+        api.lib().r4d_gemm_trellis_nt_m64_zero_tickets(buf.data_ptr(), nb, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        h = buf.cpu().numpy()
+        assert not h[:nb].any() and (h[nb:] == 0x5A).all(), nb
