@@ -45,6 +45,10 @@ def parse():
     ap.add_argument("--pmc-dense-forms", action="store_true",
                     help="counter pass for the dense int8 launch forms: 5120 x 17408 row scales, three eager launches "
                          "at SKG 1, then three in stream-K; prints no JSON line")
+    ap.add_argument("--pmc-w4", action="store_true",
+                    help="counter pass for the w4a16 LM head: a 512 MiB copy (calibration), then per group (32, 64) "
+                         "and M (1, 8) the GEMM and the fused argmax entry on two weight copies; prints the launch "
+                         "order, no JSON line")
     ap.add_argument("--pmc", action="store_true",
                     help="counter pass for rocprofv3 --pmc: a 512 MiB copy (calibration) and two eager "
                          "passes of the GEMV launches; prints no JSON line")
@@ -68,6 +72,9 @@ def main():
         return
     if args.pmc_dense_forms:
         pmc_dense_forms(api, WL)
+        return
+    if args.pmc_w4:
+        pmc_w4(api, WL)
         return
     KB, M = args.kb, args.m
     shapes = WL.LAYER_SHAPES
@@ -431,6 +438,40 @@ def bench_config1_rows(api, WL, reps=4):
                         "r4dx_trellis_gemv_xf_parts; mix = GDN and attention at KB 5, MLP at KB 4", "rows": rows}
 
 
+def pmc_w4(api, WL):
+    """The w4a16 LM head at config 3 (N = 248 320, K = 5120) for the HBM-traffic passes: a 512 MiB device copy first
+    (each counter's bytes per copied byte), then per group and M the fp32 GEMM and the fused argmax entry, each on
+    two weight copies (715 / 795 MB each, beyond the 256 MB MALL), so every launch streams its weights."""
+    import torch
+    dev = torch.device("cuda:0")
+    src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    N, K = 248320, 5120
+    order = []
+    for g in (32, 64):
+        copies = []
+        for cidx in range(2):
+            wq, wsz = WL.w4a16_packed(N, K, g, 100 + cidx)
+            copies.append((torch.from_numpy(wq.view("int32")).to(dev), torch.from_numpy(wsz.view("int32")).to(dev)))
+        for M in (1, 8):
+            a = torch.from_numpy(WL.activations_f16(M, K, 5)).to(dev)
+            out = torch.empty((M, N), dtype=torch.float32, device=dev)
+            for wq_d, wsz_d in copies:
+                api.w4a16_gemm(a, wq_d, wsz_d, K, N, g, out=out, f32=True)
+                order.append(f"g{g}_M{M}_gemm")
+            for wq_d, wsz_d in copies:
+                api.w4a16_gemm_argmax(a, wq_d, wsz_d, K, N, g, out=out)
+                order.append(f"g{g}_M{M}_fused")
+            torch.cuda.synchronize()
+        del copies
+        torch.cuda.empty_cache()
+    print(json.dumps({"pmc_pass": "done", "copy_bytes": 512 << 20, "launch_order": order}), flush=True)
+
+
 def pmc_dense_forms(api, WL):
     """The dense int8 GEMM at 5120 x 17408 (row scales) in its two launch forms, three eager launches each on one
     weight copy: SKG 1 (136 workgroups), then stream-K (256)."""
@@ -637,6 +678,13 @@ def bench_w4a16(api, WL, R=8):
     dev = torch.device("cuda:0")
     N, K = 248320, 5120
     res = {}
+    # HBM bytes over algorithmic bytes per case, from the committed summary of the two rocprofv3 --pmc passes
+    # (bench.py --pmc-w4, counters calibrated on a copy of known size); empty when absent
+    try:
+        with open(os.path.join(ROOT, "profiles", "w4a16_traffic_config3.json")) as f:
+            traffic = json.load(f).get("per_case", {})
+    except (OSError, ValueError):
+        traffic = {}
     for g in (32, 64):
         copies = []
         for cidx in range(2):
@@ -695,7 +743,8 @@ def bench_w4a16(api, WL, R=8):
                                  "frac": round(nbytes / (times[False] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                  "gemm_plus_argmax_us": round(times[True] * 1e3, 2),
                                  "argmax_alone_us": round(times[None] * 1e3, 2),
-                                 "gemm_fused_argmax_us": round(times["fused"] * 1e3, 2)}
+                                 "gemm_fused_argmax_us": round(times["fused"] * 1e3, 2),
+                                 "traffic_over_alg": traffic.get(f"g{g}_M{M}_gemm", {}).get("traffic_over_alg")}
         del copies
         torch.cuda.empty_cache()
     return {"metric": "w4a16 LM head (N=248320, K=5120) effective HBM GB/s", "kernel": "w4_kernel",
