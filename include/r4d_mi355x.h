@@ -91,9 +91,10 @@ size_t r4dx_gemm_trellis_nt_m64_noalloc_max_ws_bytes(void);
  * (two launches when SKG > 1: the slices, then their sum and the epilogue); ws fp32 ws_bytes(M, N,
  * SKG) required when SKG > 1 (the reference always requires it); tickets accepted and unused;
  * (K/16) must be divisible by 4 SKG. Every element equals, bit for bit, r4d_gemm_trellis_nt_m64's at
- * M = 64 with the same SK and SKG (r4d.h:402-412); SK must be 0, 1 or 2 (0 means 1: the one-wave-per-pair
- * order), since SK 4, 8, 16 name the 4-wave split order, which this kernel does not reproduce (_check says
- * so). NP, U, skw unused. */
+ * M = 64 with the same SK, SKG, ws and tickets (r4d.h:402-412): SK 0, 1 or 2 (0 means 1) the one-wave-per-pair
+ * order; SK 4, 8 or 16 the 4-wave split order, which (like that kernel) it runs when SKG > 1 or ws and tickets are
+ * given, else the one-wave order -- in two launches per 128-row half plus their finish passes, 1.4-1.8x the
+ * one-wave form's time, data-parallel only. Any other SK is refused. NP, U, skw unused. */
 void r4d_gemm_trellis_nt_m256(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c,
                               int64_t ws, int64_t tickets, int M, int K, int N, int KB, int SK, int NP,
                               int SKG, int U, float out_scale, int64_t stream, int skw);

@@ -142,14 +142,17 @@ def trellis_m256_skg(K, N, KB):
 
 
 def trellis_gemm_m256(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out=None, ws=None,
-                      tickets=None, out_scale=1.0, raw=False, stream=None, wq=None):
+                      tickets=None, out_scale=1.0, raw=False, stream=None, wq=None, sk=0):
     """C = r4d_gemm_trellis_nt_m256 (bf16 [M][N], M = 128 or 256) or, raw=True, fp32 A @ Q. wq = (table, gsh):
-    r4d_gemm_trellis_nt_m256_wq (bf16 only)."""
+    r4d_gemm_trellis_nt_m256_wq (bf16 only). sk: the M = 64 row's SK to reproduce (0 / 1 / 2: the one-wave order;
+    4 / 8 / 16: the 4-wave order, bf16 entries only -- the raw entry has no SK)."""
     L = lib()
     M = a0.shape[0]
     skg = trellis_m256_skg(K, N, KB) if skg is None else skg
     n_split = N if n_split is None else n_split
-    msg = L.r4d_gemm_trellis_nt_m256_check(M, K, N, n_split, KB, 0, 0, skg, 0, 0)
+    if raw and sk not in (0, 1, 2):
+        raise ValueError("r4d_gemm_trellis_nt_m256_raw computes the one-wave order only (sk 0, 1 or 2)")
+    msg = L.r4d_gemm_trellis_nt_m256_check(M, K, N, n_split, KB, sk, 0, skg, 0, 0)
     if msg:
         raise ValueError(msg.decode())
     if wq is not None:
@@ -171,13 +174,13 @@ def trellis_gemm_m256(a0, w, svh, K, N, KB, skg=None, a1=None, n_split=None, out
             raise ValueError("r4d_gemm_trellis_nt_m256_wq has no raw form")
         tab, gsh = _wq_args(wq, K, KB)
         L.r4d_gemm_trellis_nt_m256_wq(_p(a0), _p(a1), n_split, _p(w), _p(svh), _p(out), _p(ws), _p(tickets),
-                                      M, K, N, KB, 0, 0, skg, 0, float(out_scale), st, 0, tab, gsh)
+                                      M, K, N, KB, sk, 0, skg, 0, float(out_scale), st, 0, tab, gsh)
     elif raw:
         L.r4d_gemm_trellis_nt_m256_raw(_p(a0), _p(a1), n_split, _p(w), _p(out), _p(ws), _p(tickets),
                                        M, K, N, KB, skg, st)
     else:
         L.r4d_gemm_trellis_nt_m256(_p(a0), _p(a1), n_split, _p(w), _p(svh), _p(out), _p(ws), _p(tickets),
-                                   M, K, N, KB, 0, 0, skg, 0, float(out_scale), st, 0)
+                                   M, K, N, KB, sk, 0, skg, 0, float(out_scale), st, 0)
     return out
 
 

@@ -97,7 +97,11 @@ __device__ __forceinline__ M2Seg m2_seg(const M2Share& sh, int si, int nst) {
   return g;
 }
 
-template <int KB, int RT, bool WQ = false>
+// SK4: the M <= 64 kernel's 4-wave order (its SK 4, 8 and 16): each K slice's steps are cut into 4 contiguous parts of
+// ceil(steps / 4) steps, each part summed from 0.f, the parts added in order ((p0 + p1) + p2) + p3 (an empty part adds
+// +0.f); the slice then always goes through ws (or raw C) and tq_m256_finish, as that kernel's split hand-over does.
+// Data-parallel only (P = 0), and with RT = 4: the finished parts' sum takes a second accumulator set.
+template <int KB, int RT, bool WQ = false, bool SK4 = false>
 __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
     const R4AParts ap, const unsigned* __restrict__ W, const float* __restrict__ svh, void* __restrict__ Cv,
     float* __restrict__ ws, int M, int K, int N, int SKG, int full, float out_scale,
@@ -252,7 +256,7 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
       // the math waves' closing barriers: the publish handoff, or the epilogue's two exchange rounds
       if (kind == kSegPublish) {
         __syncthreads();
-      } else if (SKG == 1 && full) {
+      } else if (SKG == 1 && full && !SK4) {
 #pragma unroll 1
         for (int r = 0; r < 2 * 2; ++r) __syncthreads();
       }
@@ -272,6 +276,23 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
     const int rh = wave >> 1, ch = wave & 1;
     const int r16 = lane_s & 15, g = lane_s >> 4;
     r4f4 acc[RT][4];
+    r4f4 tot[SK4 ? RT : 1][4];                     // SK4: the sum of the finished parts
+    const int nsw = SK4 ? (ns + 3) / 4 : 0;        // SK4: steps per part
+    int next_part = nsw, folds = 0;
+    // SK4, at a part boundary: tot = p0, then tot + p1, ...; the next part starts from 0.f
+    auto fold = [&]() {
+#pragma unroll
+      for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          if constexpr (SK4) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) tot[i][ct][j] = folds == 0 ? acc[i][ct][j] : tot[i][ct][j] + acc[i][ct][j];
+          }
+          acc[i][ct] = (r4f4){0.f, 0.f, 0.f, 0.f};
+        }
+      ++folds;
+    };
     // a published slot is [wave][i][ct][lane_s] r4f4: one coalesced 1 KiB run per (wave, i, ct)
     if (kind == kSegContinue) {
       // coherent (sc1) 16-byte loads: one per (i, ct), lane_s-contiguous, offsets constant past the lane_s's own
@@ -320,10 +341,30 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
       __builtin_amdgcn_s_barrier();                        // B_(st+1): stage st + 1 landed
       read_half(af0, bf0, st + 1, 0);
       mfma_half(af1, bf1);
+      if constexpr (SK4) {
+        if (st + 1 == next_part) {   // step st closed a part (uniform: a scalar branch)
+          fold();
+          next_part += nsw;
+        }
+      }
     }
     read_half(af1, bf1, ns - 1, 1);
     mfma_half(af0, bf0);
     mfma_half(af1, bf1);
+    if constexpr (SK4) {
+      // the last part added to the others; fewer than 4 non-empty parts: the empty ones' +0.f (once is all of them)
+      const bool empty = (ns + nsw - 1) / nsw < 4;
+#pragma unroll
+      for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float v = folds > 0 ? tot[i][ct][j] + acc[i][ct][j] : acc[i][ct][j];
+            if (empty) v = v + 0.f;
+            acc[i][ct][j] = v;
+          }
+    }
 
     if (kind == kSegPublish) {
       // coherent (sc1, write-through) 16-byte stores in the layout the continuation reads
@@ -353,8 +394,8 @@ __global__ __launch_bounds__(64 * kM2Waves, 1) void tq_m256_kernel(
     // reads element 0 whatever j is.)
     unsigned nvv = (unsigned)Nv;
     asm volatile("" : "+v"(nvv));
-    if (SKG > 1 || !full) {
-      float* dst = SKG > 1 ? ws + (size_t)ky * M * Nv : (float*)Cv;
+    if (SK4 || SKG > 1 || !full) {
+      float* dst = SKG > 1 || (SK4 && full) ? ws + (size_t)ky * M * Nv : (float*)Cv;
       const r4_rsrc dr = mk_rsrc(dst, (unsigned)((size_t)M * Nv * 4));
 #pragma unroll
       for (int i = 0; i < RT; ++i)
@@ -553,24 +594,48 @@ int m256_balanced_p(int M, int N, int SKG, bool have_ws, bool have_tickets) {
   return cus;
 }
 
-template <int KB, int RT, bool WQ>
+template <int KB, int RT, bool WQ, bool SK4 = false>
 void m256_launch_rt(const R4AParts& ap, const unsigned* w,
                     const float* svh, void* c, float* ws, unsigned* tickets, int M, int K, int N, int SKG, int full,
                     float out_scale, const float* wsc, int wq_gsh, hipStream_t st) {
   constexpr unsigned lds = 2 * (32 * RT * 128 + 128 * 128);
   static std::atomic<unsigned long long> lds_set{0};
-  r4d::allow_lds((const void*)tq_m256_kernel<KB, RT, WQ>, lds_set, "gemm_trellis_nt_m256");
-  const int P = m256_balanced_p(M, N, SKG, ws != nullptr, tickets != nullptr);
+  r4d::allow_lds((const void*)tq_m256_kernel<KB, RT, WQ, SK4>, lds_set, "gemm_trellis_nt_m256");
+  const int P = SK4 ? 0 : m256_balanced_p(M, N, SKG, ws != nullptr, tickets != nullptr);
   // the published accumulators follow the SKG slices in ws (SKG = 1: no slices, they start at ws)
   float* fix = ws ? ws + (SKG > 1 ? (size_t)SKG * M * N : 0) : nullptr;
   const dim3 grid = P > 0 ? dim3(P) : dim3(N / 128, SKG);
-  hipLaunchKernelGGL((tq_m256_kernel<KB, RT, WQ>), grid, dim3(64 * kM2Waves), lds, st, ap,
+  hipLaunchKernelGGL((tq_m256_kernel<KB, RT, WQ, SK4>), grid, dim3(64 * kM2Waves), lds, st, ap,
                      w, svh, c, ws, M, K, N, SKG, full, out_scale, wsc, wq_gsh, fix, tickets, P);
 }
+// The SK4 order, one launch per 128-row half (the 128-row form holds the second accumulator set): half h reads its
+// parts' rows from 128 h, writes C's rows from 128 h (bf16, or fp32 raw) and, through ws, its own [SKG][128][N]
+// slices -- ws holds both halves' slices in SKG M N floats -- each finished by its own second pass.
+template <int KB, bool WQ>
+void m256_launch_sk4(int M, const R4AParts& ap, const unsigned* w, const float* svh, void* c, float* ws, int K, int N,
+                     int SKG, int full, float out_scale, const float* wsc, int wq_gsh, hipStream_t st) {
+  for (int h = 0; h < M / 128; ++h) {
+    R4AParts aph = ap;
+    for (int p = 0; p < 4; ++p) aph.a[p] = ap.a[p] + (size_t)h * 128 * K;
+    void* ch = (char*)c + (size_t)h * 128 * N * (full ? 2 : 4);
+    float* wsh = ws ? ws + (size_t)h * SKG * 128 * N : nullptr;
+    m256_launch_rt<KB, 4, WQ, true>(aph, w, svh, ch, wsh, nullptr, 128, K, N, SKG, full, out_scale, wsc, wq_gsh, st);
+    if (SKG > 1 || full) r4d::launch_split_finish(wsh, svh, ch, 128, N, SKG, full, out_scale, st);
+  }
+}
+
 template <int KB>
 void m256_launch(int M, const R4AParts& ap, const unsigned* w,
                  const float* svh, void* c, float* ws, unsigned* tickets, int K, int N, int SKG, int full,
-                 float out_scale, const float* wsc, int wq_gsh, hipStream_t st) {
+                 float out_scale, const float* wsc, int wq_gsh, hipStream_t st, bool sk4) {
+  if (sk4) {
+    if (wsc) {
+      if constexpr (KB == 4 || KB == 5) m256_launch_sk4<KB, true>(M, ap, w, svh, c, ws, K, N, SKG, full, out_scale, wsc, wq_gsh, st);
+    } else {
+      m256_launch_sk4<KB, false>(M, ap, w, svh, c, ws, K, N, SKG, full, out_scale, nullptr, 0, st);
+    }
+    return;
+  }
   if (wsc) {
     if constexpr (KB == 4 || KB == 5) {
       if (M == 256) m256_launch_rt<KB, 8, true>(ap, w, svh, c, ws, tickets, M, K, N, SKG, full, out_scale, wsc, wq_gsh, st);
@@ -582,32 +647,35 @@ void m256_launch(int M, const R4AParts& ap, const unsigned* w,
   else m256_launch_rt<KB, 4, false>(ap, w, svh, c, ws, tickets, M, K, N, SKG, full, out_scale, nullptr, 0, st);
 }
 
+// sk_split: the caller asked for the M <= 64 kernel's 4-wave order (SK 4, 8, 16), which that kernel runs when SKG > 1
+// or ws and tickets are given (else its one-wave form).
 void m256_run_parts(const R4AParts& ap, int64_t w, int64_t svh, int64_t c, int64_t ws, int64_t tickets, int M,
                     int K, int N, int KB, int SKG, int full, float out_scale, int64_t stream, const char* entry,
-                    int64_t wscale = 0, int wq_gsh = 0) {
+                    int64_t wscale = 0, int wq_gsh = 0, bool sk_split = false) {
   r4d::require(entry, m256_check(M, K, N, ap.n_end[0] > N ? N : ap.n_end[0], KB, SKG));
   if (!ap.a[0] || !w || !c) r4d::fail(entry, "null A, W or C");
   if (full && !svh) r4d::fail(entry, "svh must be non-null");
   if (SKG > 1 && !ws) r4d::fail(entry, "SKG > 1 needs ws");
+  const bool sk4 = sk_split && (SKG > 1 || (ws && tickets));
   auto Wp = (const unsigned*)w;
   auto S = (const float*)svh;
   auto WS = (float*)ws;
   auto T = (unsigned*)tickets;
   hipStream_t st = (hipStream_t)stream;
   auto WSC = (const float*)wscale;
-  if (KB == 4) m256_launch<4>(M, ap, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st);
-  else if (KB == 5) m256_launch<5>(M, ap, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st);
-  else m256_launch<3>(M, ap, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st);
-  if (SKG > 1) r4d::launch_split_finish(WS, S, (void*)c, M, N, SKG, full, out_scale, st);
+  if (KB == 4) m256_launch<4>(M, ap, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st, sk4);
+  else if (KB == 5) m256_launch<5>(M, ap, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st, sk4);
+  else m256_launch<3>(M, ap, Wp, S, (void*)c, WS, T, K, N, SKG, full, out_scale, WSC, wq_gsh, st, sk4);
+  if (SKG > 1 && !sk4) r4d::launch_split_finish(WS, S, (void*)c, M, N, SKG, full, out_scale, st);
   r4d::launch_ok(entry);
 }
 
 void m256_run(int64_t a0, int64_t a1, int n_split, int64_t w, int64_t svh, int64_t c, int64_t ws,
               int64_t tickets, int M, int K, int N, int KB, int SKG, int full, float out_scale, int64_t stream,
-              const char* entry, int64_t wscale = 0, int wq_gsh = 0) {
+              const char* entry, int64_t wscale = 0, int wq_gsh = 0, bool sk_split = false) {
   r4d::require(entry, m256_check(M, K, N, n_split, KB, SKG));
   m256_run_parts(r4_parts((const void*)a0, (const void*)a1, n_split), w, svh, c, ws, tickets, M, K, N, KB, SKG, full,
-                 out_scale, stream, entry, wscale, wq_gsh);
+                 out_scale, stream, entry, wscale, wq_gsh, sk_split);
 }
 
 }  // namespace
@@ -618,11 +686,13 @@ void r4d::launch_split_finish(const float* ws, const float* svh, void* c, int M,
 }
 
 // SK names the M <= 64 row this launch reproduces: 1 or 2 (0 means 1) is r4d_gemm_trellis_nt_m64's one-wave-per-pair
-// order, the only one this kernel computes; 4, 8 and 16 name the 4-wave split order.
-static bool m256_sk_ok(int SK) { return SK == 0 || SK == 1 || SK == 2; }
+// order; 4, 8 and 16 its 4-wave split order (which that kernel runs when SKG > 1 or ws and tickets are given, else its
+// one-wave form -- and so does this one).
+static bool m256_sk_ok(int SK) { return SK == 0 || SK == 1 || SK == 2 || SK == 4 || SK == 8 || SK == 16; }
+static bool m256_sk_split(int SK) { return SK == 4 || SK == 8 || SK == 16; }
 static const char* const sk_msg =
-    "SK must be 1 or 2 (0 means 1): the M <= 64 row this reproduces is r4d_gemm_trellis_nt_m64's one-wave-per-pair "
-    "order (its SK 1 and 2); SK 4, 8 and 16 name the 4-wave split order, which this kernel does not compute";
+    "SK must be 1, 2, 4, 8 or 16 (0 means 1): 1 and 2 reproduce r4d_gemm_trellis_nt_m64's one-wave-per-pair order, "
+    "4, 8 and 16 its 4-wave split order";
 
 extern "C" {
 
@@ -636,7 +706,7 @@ void r4d_gemm_trellis_nt_m256(int64_t a0, int64_t a1, int n_split, int64_t w, in
   (void)NP; (void)U; (void)skw;
   if (!m256_sk_ok(SK)) r4d::fail("gemm_trellis_nt_m256", sk_msg);
   m256_run(a0, a1, n_split, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale, stream,
-           "gemm_trellis_nt_m256");
+           "gemm_trellis_nt_m256", 0, 0, m256_sk_split(SK));
 }
 
 const char* r4d_gemm_trellis_nt_m256_check(int M, int K, int N, int n_split, int KB, int SK, int NP, int SKG,
@@ -696,7 +766,8 @@ void r4d_gemm_trellis_nt_m256_wq(int64_t a0, int64_t a1, int n_split, int64_t w,
   if (!wscale) r4d::fail(e, "the _wq entry needs a scale table (r4d_trellis_wscale_f32)");
   if (gsh < 1 || gsh > 3 || K % (16 << gsh)) r4d::fail(e, "gsh must be 1, 2 or 3 with 16 << gsh dividing K");
   if (KB != 4 && KB != 5) r4d::fail(e, "KB must be 4 or 5");
-  m256_run(a0, a1, n_split, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale, stream, e, wscale, gsh);
+  m256_run(a0, a1, n_split, w, svh, c, ws, tickets, M, K, N, KB, SKG, 1, out_scale, stream, e, wscale, gsh,
+           m256_sk_split(SK));
 }
 
 // This build's K split for the prefill GEMM: the steps per CU decide the critical path (one workgroup resident per

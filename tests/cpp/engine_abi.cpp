@@ -59,13 +59,15 @@ void cpu_checks() {
     r4d_gemm_trellis_nt_m64(kFake, 0, 256, kFake, kFake, kFake, 0, 0, 1, 512, 256, 4, 0, 0, 0, 0, 2, 0, 0, 1.f, 0);
   });
   expect(!e2.empty(), "m64 throws on SKG 2 without ws");
-  // the M = 256 GEMM computes the one-wave-per-pair order only: SK 4 is refused
-  expect(r4d_gemm_trellis_nt_m256_check(256, 512, 256, 256, 4, 4, 0, 1, 0, 0) != nullptr, "m256_check refuses SK 4");
+  // the M = 256 GEMM reproduces the M = 64 row of SK 1 / 2 (one wave per pair) and SK 4 / 8 / 16 (4-wave split);
+  // any other SK is refused
+  expect(r4d_gemm_trellis_nt_m256_check(256, 512, 256, 256, 4, 3, 0, 1, 0, 0) != nullptr, "m256_check refuses SK 3");
   const std::string e3 = thrown([] {
-    r4d_gemm_trellis_nt_m256(kFake, 0, 256, kFake, kFake, kFake, kFake, 0, 256, 512, 256, 4, 4, 0, 1, 0, 1.f, 0, 0);
+    r4d_gemm_trellis_nt_m256(kFake, 0, 256, kFake, kFake, kFake, kFake, 0, 256, 512, 256, 4, 3, 0, 1, 0, 1.f, 0, 0);
   });
-  expect(!e3.empty(), "m256 throws on SK 4");
+  expect(!e3.empty(), "m256 throws on SK 3");
   expect(r4d_gemm_trellis_nt_m256_check(256, 512, 256, 256, 4, 1, 0, 1, 0, 0) == nullptr, "m256_check accepts SK 1");
+  expect(r4d_gemm_trellis_nt_m256_check(256, 512, 256, 256, 4, 4, 0, 1, 0, 0) == nullptr, "m256_check accepts SK 4");
   expect(r4d_gemm_trellis_nt_m64_tickets_bytes(5120) == 40 * 128, "tickets_bytes: one 128-byte line per group");
   expect(r4d_gemm_trellis_nt_m64_ws_bytes(8, 5120, 4) == (size_t)4 * 8 * 5120 * 4, "ws_bytes = SKG M N fp32");
   expect(r4d_gemm_trellis_nt_m64_has_rate(4) && r4d_gemm_trellis_nt_m64_has_rate(5) &&
@@ -208,6 +210,20 @@ void gpu_checks() {
     same = same && std::memcmp(c64.data(), c256.data() + (size_t)r0 * N, c64.size() * 2) == 0;
   }
   expect(same, "M = 256 rows == M = 64 rows at SK 1, SKG 2, bit for bit");
+  // the same at SK 4 (the 4-wave split order; ws and tickets given to both)
+  r4d_gemm_trellis_nt_m256(da256.a(), 0, N, dw.a(), dsvh.a(), dc256.a(), dws256.a(), dtk256.a(), MB, K, N, KB, 4, 0,
+                           SKG, 0, out_scale, s, 0);
+  HIPCHECK(hipStreamSynchronize(st));
+  const std::vector<uint16_t> c256s = dc256.get<uint16_t>((size_t)MB * N);
+  same = true;
+  for (int r0 = 0; r0 < MB; r0 += 64) {
+    r4d_gemm_trellis_nt_m64(da256.a() + (int64_t)r0 * K * 2, 0, N, dw.a(), dsvh.a(), dc64.a(), dws64.a(), dtk.a(), 64,
+                            K, N, KB, 0, 4, 0, 0, SKG, 0, 0, out_scale, s);
+    HIPCHECK(hipStreamSynchronize(st));
+    const std::vector<uint16_t> c64 = dc64.get<uint16_t>((size_t)64 * N);
+    same = same && std::memcmp(c64.data(), c256s.data() + (size_t)r0 * N, c64.size() * 2) == 0;
+  }
+  expect(same, "M = 256 rows == M = 64 rows at SK 4, SKG 2, bit for bit");
 
   // 6. w4a16 at group 64 (quant_int4.hpp's quantizer and packers), then the argmax of its fp32 logits
   {

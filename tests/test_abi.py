@@ -90,10 +90,12 @@ def test_m256_checks(L):
     assert ck(128, 5120, 5120, 5120, 5, 0, 0, 1, 0, 0) is None
     assert b"M must be" in ck(64, 5120, 5120, 5120, 4, 0, 0, 1, 0, 0)
     assert b"SKG" in ck(256, 5120, 5120, 5120, 4, 0, 0, 3, 0, 0)
-    # SK 1 and 2 name the M = 64 one-wave-per-pair order this kernel reproduces; 4, 8, 16 the split order
+    # SK 1 and 2 name the M = 64 one-wave-per-pair order, 4, 8 and 16 its 4-wave split order: both reproduced
     assert ck(256, 5120, 5120, 5120, 4, 2, 1, 2, 4, 2) is None and ck(256, 5120, 5120, 5120, 4, 1, 1, 2, 4, 0) is None
     for sk in (4, 8, 16):
-        assert b"SK must be 1 or 2" in ck(256, 5120, 5120, 5120, 4, sk, 1, 2, 4, 4)
+        assert ck(256, 5120, 5120, 5120, 4, sk, 1, 2, 4, 4) is None
+    for sk in (3, 32):
+        assert b"SK must be 1, 2, 4, 8 or 16" in ck(256, 5120, 5120, 5120, 4, sk, 1, 2, 4, 4)
     # SKG slices, then (SKG > 1) the balanced form's hand-over area: M x 128 fp32 for each of min(units, CUs)
     # workgroups (no GPU here: 256 CUs assumed); SKG = 1 needs no more than the M x N floats
     assert L.r4d_gemm_trellis_nt_m256_ws_bytes(256, 5120, 2) == 2 * 256 * 5120 * 4 + 80 * 256 * 128 * 4

@@ -76,11 +76,72 @@ def test_m256_bit_identical_to_m64_rows(M, K, N, KB, skg):
         assert torch.equal(big[sl].view(torch.int16), small.view(torch.int16)), r0
 
 
-def test_m256_rejects_sk_above_1():
+@pytest.mark.parametrize("M,K,N,KB,skg,sk", [
+    (256, 1024, 384, 4, 1, 4),     # 16 steps per slice: 4 parts of 4 (SKG 1: the slice through ws and the finish)
+    (256, 1152, 256, 4, 2, 8),     # 9 steps: parts of 3, 3, 3 and an empty one
+    (128, 640, 256, 5, 1, 16),     # 10 steps: 3, 3, 3, 1
+    (256, 2048, 256, 3, 8, 4),     # 4 steps: one each
+    (256, 1024, 256, 4, 16, 4),    # 1 step: one part, three empty (16 slices: the finish's interleaved runs)
+    (256, 5120, 640, 4, 4, 4),     # two A parts
+])
+def test_m256_sk4_bit_identical_to_m64_rows(M, K, N, KB, skg, sk):
+    """SK 4, 8 and 16 (r4d.h:406: the M = 64 row's K-slice count to reproduce): the M <= 64 kernel's 4-wave order (each
+    slice's steps in 4 contiguous parts, each from 0.f, added in order), with ws and tickets given -- every element of
+    the M = 256 (128) launch equals, bit for bit, the M = 64 launch with the same SK, SKG, ws and tickets, one 64-row
+    chunk at a time (bf16 and the _wq fake-quant form)."""
+    banner("m256 sk4 == m64", M, K, N, KB, skg, sk)
+    words, _, svh = WL.trellis_linear(K, N, KB, 5 * K + skg)
+    a = WL.activations_f16(M, K, 27, outlier_frac=0.01).view(np.uint16)
+    a1 = WL.activations_f16(M, K, 28).view(np.uint16)
+    w_d, a_d, a1_d, s_d = dev(words), dev(a), dev(a1), dev(svh)
+    ns = N // 2 if N % 256 == 0 else N
+    osc = float(np.float32(1.0 / np.sqrt(128.0)))
+    big = api.trellis_gemm_m256(a_d, w_d, s_d, K, N, KB, skg=skg, a1=a1_d, n_split=ns, out_scale=osc, sk=sk)
+    wq = None
+    if KB in (4, 5) and (K // 16) % 4 == 0 and K % 32 == 0:
+        wq = (api.trellis_wscale(w_d, K, N, KB, 1), 1)
+        big_wq = api.trellis_gemm_m256(a_d, w_d, s_d, K, N, KB, skg=skg, a1=a1_d, n_split=ns, out_scale=osc, sk=sk,
+                                       wq=wq)
+    for r0 in range(0, M, 64):
+        sl = slice(r0, r0 + 64)
+        ws = torch.empty(api.lib().r4d_gemm_trellis_nt_m64_ws_bytes(64, N, skg) // 4, dtype=torch.float32,
+                         device="cuda")
+        tk = api.TicketBuffer(N).t
+        small = api.trellis_gemm_m64(a_d[sl].contiguous(), w_d, s_d, K, N, KB, skg=skg, a1=a1_d[sl].contiguous(),
+                                     n_split=ns, out_scale=osc, sk=sk, ws=ws, tickets=tk)
+        torch.cuda.synchronize()
+        assert torch.equal(big[sl].view(torch.int16), small.view(torch.int16)), r0
+        if wq is not None:
+            small_wq = api.trellis_gemm_m64(a_d[sl].contiguous(), w_d, s_d, K, N, KB, skg=skg,
+                                            a1=a1_d[sl].contiguous(), n_split=ns, out_scale=osc, sk=sk, ws=ws,
+                                            tickets=tk, wq=wq)
+            torch.cuda.synchronize()
+            assert torch.equal(big_wq[sl].view(torch.int16), small_wq.view(torch.int16)), r0
+
+
+def test_m256_sk4_without_ws_runs_the_one_wave_order():
+    """SK 4 at SKG 1 with no ws and no tickets: the M <= 64 kernel runs its one-wave form there, and so does the M = 256
+    launch -- the same bits as SK 1."""
+    banner("m256 sk4 no ws")
+    M, K, N, KB = 256, 1024, 256, 4
+    words, _, svh = WL.trellis_linear(K, N, KB, 77)
+    a_d, w_d, s_d = dev(WL.activations_f16(M, K, 78).view(np.uint16)), dev(words), dev(svh)
+    osc = float(np.float32(1.0 / np.sqrt(128.0)))
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    api.lib().r4d_gemm_trellis_nt_m256(a_d.data_ptr(), 0, N, w_d.data_ptr(), s_d.data_ptr(), out.data_ptr(), 0, 0,
+                                       M, K, N, KB, 4, 0, 1, 0, osc, torch.cuda.current_stream().cuda_stream, 0)
+    one = api.trellis_gemm_m256(a_d, w_d, s_d, K, N, KB, skg=1, out_scale=osc, sk=1)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), one.view(torch.int16))
+
+
+def test_m256_sk_rule():
     L = api.lib()
-    assert L.r4d_gemm_trellis_nt_m256_check(256, 1024, 256, 256, 4, 1, 0, 1, 0, 0) is None
-    msg = L.r4d_gemm_trellis_nt_m256_check(256, 1024, 256, 256, 4, 4, 0, 1, 0, 0)
-    assert msg and b"SK" in msg
+    for sk in (0, 1, 2, 4, 8, 16):
+        assert L.r4d_gemm_trellis_nt_m256_check(256, 1024, 256, 256, 4, sk, 0, 1, 0, 0) is None, sk
+    for sk in (3, 5, 32):
+        msg = L.r4d_gemm_trellis_nt_m256_check(256, 1024, 256, 256, 4, sk, 0, 1, 0, 0)
+        assert msg and b"SK" in msg, sk
 
 
 def test_m256_two_part():

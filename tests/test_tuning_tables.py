@@ -184,12 +184,11 @@ REF_TABLE = "/root/reference/src/model/gemm_tuning_table_trellis.inc"
 
 
 @pytest.mark.skipif(not os.path.exists(REF_TABLE), reason="the reference checkout is not here")
-def test_reference_rdna4_rows_split_order_refused():
-    """The M = 256 kernel computes the one-wave-per-pair order only (SK 1 or 2 in the reference's terms,
-    r4d.h:402-412). An engine still on the reference's own RDNA4 table (src/model/gemm_tuning_table_trellis.inc) plans
-    the M = 256 launch from the M = 64 row (linear.cpp:680-724): every such row with SK 4, 8 or 16 is refused with the
-    documented message, and the planner then returns no plan (the engine runs the chunk as M <= 64 launches); a row with
-    SK 1 or 2 plans as it does on this build's tables."""
+def test_reference_rdna4_rows_plan_the_m256_launch():
+    """An engine still on the reference's own RDNA4 table (src/model/gemm_tuning_table_trellis.inc) plans the M = 256
+    launch from the M = 64 row (linear.cpp:680-724). Every such row -- SK 1 or 2 (the one-wave-per-pair order) or SK
+    4, 8, 16 (the 4-wave split order, r4d.h:406) -- passes the kernel's _check wherever its SKG divides the shape, and
+    the planner returns a plan for it."""
     rows = _trellis_rows(None, REF_TABLE)
     ck = lib().r4d_gemm_trellis_nt_m256_check
     seen = {1: 0, 2: 0, 4: 0, 8: 0, 16: 0}
@@ -198,13 +197,10 @@ def test_reference_rdna4_rows_split_order_refused():
             continue
         t, kb, N, K = r["t"], r["rate"], r["N"], r["K"]
         seen[t["SK"]] += 1
-        for skw in (2, 4, 8):
-            msg = ck(256, K, N, N, kb, t["SK"], 1, t["SKG"], 4, skw)
-            if t["SK"] >= 4:
-                assert msg is not None and b"SK must be 1 or 2" in msg, (N, K, kb, t)
+        legal = ck(256, K, N, N, kb, t["SK"], 1, t["SKG"], 4, 2) is None
+        if (K // 16) % (4 * t["SKG"]) == 0:
+            assert legal, (N, K, kb, t)
         planned, _ = plan_m256(rows, N, K, kb)
-        if t["SK"] >= 4:
-            assert planned is None, (N, K, kb, t)
-        elif ck(256, K, N, N, kb, t["SK"], 1, t["SKG"], 4, 2) is None:
+        if legal:
             assert planned is not None, (N, K, kb, t)
     assert seen[4] + seen[8] + seen[16] > 0 and sum(seen.values()) > 0
