@@ -83,9 +83,11 @@ def test_graph_gemv_parts_and_fused():
     _replays("gemv xf parts", fused, lambda v: [out[v]])
 
 
-@pytest.mark.parametrize("M,K,N,kb,skg", [(256, 2048, 512, 4, 2), (128, 1024, 33024, 5, 1)])
-def test_graph_m256(M, K, N, kb, skg):
-    """A split launch (slices + the finish launch) and a balanced one (cut units handed over through flags)."""
+@pytest.mark.parametrize("M,K,N,kb,skg,sk", [(256, 2048, 512, 4, 2, 0), (128, 1024, 33024, 5, 1, 0),
+                                             (256, 1152, 512, 4, 2, 4)])
+def test_graph_m256(M, K, N, kb, skg, sk):
+    """A split launch (slices + the finish launch), a balanced one (cut units handed over through flags), and the 4-wave
+    split order (SK 4: a launch and a finish per 128-row half)."""
     words, _, svh = WL.trellis_linear(K, N, kb, 21)
     w_d, svh_d = dev(words), dev(svh)
     a = [dev(WL.activations_f16(M, K, 22 + v)) for v in (0, 1)]
@@ -95,8 +97,8 @@ def test_graph_m256(M, K, N, kb, skg):
 
     def run(v):
         api.trellis_gemm_m256(a[v], w_d, svh_d, K, N, kb, skg=skg, out=out[v], ws=ws, tickets=tickets,
-                              out_scale=OUT_SCALE)
-    _replays(f"m256 M={M} N={N} skg={skg}", run, lambda v: [out[v]])
+                              out_scale=OUT_SCALE, sk=sk)
+    _replays(f"m256 M={M} N={N} skg={skg} sk={sk}", run, lambda v: [out[v]])
 
 
 def test_graph_trellis_i8_and_dense_int8():
