@@ -341,6 +341,9 @@ def main():
                    "M": M, "KB": KB, "weight_bytes_per_step": layer_wbytes,
                    "step": "6 input transforms (shared by projections with the same input, nout 1-3) + 6 trellis "
                            "GEMV launches (FWHT/svh epilogue, bf16 out); every weight byte of the layer read once",
+                   "timing": f"HIP-graph replays (one sweep over the weight copies each), {args.warmup} untimed warm-up "
+                             f"steps right before the {steps} timed ones; every other timed graph after "
+                             f"{WARM_REPLAYS} warm-up replays",
                    "median_of_11_rounds_ms_per_step": round(ms_round_med, 4),
                    "median_of_11_rounds_GBs": round(layer_wbytes / (ms_round_med * 1e-3) / 1e9, 1),
                    "per_projection_ms_per_step": round(ms_step_proj, 4),
