@@ -621,7 +621,7 @@ def bench_m256(api, WL, KB, R=3):
     # config 1's 4/5 mix.
     shape = {name: (K, N) for name, K, N in WL.LAYER_SHAPES}
 
-    def layer(kb_of):
+    def layer(kb_of, Mr=M):
         per_launch, tot_flop, tot_ms = {}, 0.0, 0.0
         for i, (gname, members) in enumerate(WL.LAYER_GROUPS):
             KBg = kb_of(gname)
@@ -633,14 +633,14 @@ def bench_m256(api, WL, KB, R=3):
             nw = K * N * KBg // 32
             copies = max(2, int(np.ceil(1.0e9 / (nw * 4))))
             words = [torch.randint(-2**31, 2**31 - 1, (nw,), dtype=torch.int32, device=dev) for _ in range(copies)]
-            a = [torch.from_numpy(WL.activations_f16(M, K, 60 + 4 * i + j, outlier_frac=0.01)).to(dev)
+            a = [torch.from_numpy(WL.activations_f16(Mr, K, 60 + 4 * i + j, outlier_frac=0.01)).to(dev)
                  for j in range(len(names))]
             svh = torch.from_numpy(WL.svh_scales(N, 70 + i)).to(dev)
             skg = api.trellis_m256_skg(K, N, KBg)
-            ws = torch.empty(api.lib().r4d_gemm_trellis_nt_m256_ws_bytes(M, N, skg) // 4, dtype=torch.float32,
+            ws = torch.empty(api.lib().r4d_gemm_trellis_nt_m256_ws_bytes(Mr, N, skg) // 4, dtype=torch.float32,
                              device=dev)
             tk = api.TicketBuffer(N, dev).t
-            out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            out = torch.empty((Mr, N), dtype=torch.bfloat16, device=dev)
 
             def run():
                 for c in range(copies):
@@ -668,7 +668,7 @@ def bench_m256(api, WL, KB, R=3):
             e1.record(st)
             torch.cuda.synchronize()
             ms = e0.elapsed_time(e1) / (R * copies)
-            flop = 2.0 * M * K * N
+            flop = 2.0 * Mr * K * N
             per_launch["|".join(names)] = {"us": round(ms * 1e3, 2), "TFLOPs": round(flop / (ms * 1e-3) / 1e12, 1),
                                            "skg": skg, "KB": KBg}
             tot_flop += flop
@@ -680,8 +680,9 @@ def bench_m256(api, WL, KB, R=3):
     per_launch, tot_flop, tot_ms = layer(lambda g: KB)
     rows = {}
     if KB == 4:
-        for rate, kb_of in (("KB5", lambda g: 5), ("mix", lambda g: 5 if g in MIX_KB5 else 4)):
-            pl, fl, t = layer(kb_of)
+        for rate, kb_of, mr in (("KB5", lambda g: 5, M), ("mix", lambda g: 5 if g in MIX_KB5 else 4, M),
+                                ("M128", lambda g: 4, 128)):
+            pl, fl, t = layer(kb_of, mr)
             rows[rate] = {"layer_us": round(t * 1e3, 1), "TFLOPs": round(fl / (t * 1e-3) / 1e12, 1),
                           "per_launch_us": {k: v["us"] for k, v in pl.items()}}
     achieved = tot_flop / (tot_ms * 1e-3) / 1e12
@@ -693,8 +694,8 @@ def bench_m256(api, WL, KB, R=3):
             "workload": "config2: the layer's 10 projections as 6 launches (same-input projections as one linear)",
             "layer_us": round(tot_ms * 1e3, 1), "per_launch": per_launch,
             "per_projection_TFLOPs": round(per_proj, 1), "per_shape": per_shape,
-            "rows": {"workload": "the same 6-launch layer at KB 5, and at config 1's 4/5 mix (GDN and attention at "
-                                 "KB 5, the MLP at KB 4)", "rows": rows}}
+            "rows": {"workload": "the same 6-launch layer at KB 5, at config 1's 4/5 mix (GDN and attention at "
+                                 "KB 5, the MLP at KB 4), and at M = 128 (KB 4; the 128-row form)", "rows": rows}}
 
 
 def bench_w4a16(api, WL, R=8):
